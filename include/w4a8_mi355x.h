@@ -1,0 +1,115 @@
+/*
+ * w4a8_mi355x.h -- C ABI of libw4a8_mi355x.so, the MI355X (gfx950) W4A8 quantized-linear path.
+ *
+ * Drop-in boundary for minisglang-rdna4's W4A8 hot path. The reference calls three external HIP
+ * packages from its Python provider (python/minisgl/quant/kernels.py): fp8_wmma (GEMM/GEMV core),
+ * moe_hip (route + align) and tail_hip (act-quant epilogues). Each entry point below names the
+ * reference interface it replaces. Conventions:
+ *   - plain device pointers, sizes and a hipStream_t passed as void*; no framework types;
+ *   - every function returns 0 on success, otherwise a status code, and w4a8_last_error() returns
+ *     the message of the calling thread's last failure (argument errors are detected on the host
+ *     before any launch);
+ *   - no entry point allocates: outputs and workspaces come from the caller, so every launch is
+ *     capturable into a HIP graph as long as its pointers stay fixed;
+ *   - dtype codes: 0 = bf16, 1 = fp16, 2 = f32. Scale formats: 0 = fp16 group scales,
+ *     1 = E8M0 (uint8) 32-element block scales. Weight formats: 0 = int4 codes, 1 = e2m1 codes.
+ *
+ * Data layouts (all row-major):
+ *   x_fp8 (M, ldx) uint8 e4m3fn codes; act_scales (M,) f32.
+ *   w_packed (N, K/8) int32 -- the reference op layout: nibble j of word k/8 is input k.
+ *   w_tile: the W4 tile layout written by w4a8_repack_weights, w4a8_tile_bytes(N, K) bytes.
+ *   scales (K/group, N) group-major; zeros (K/group, N/8) int32, 8 channels per word, or NULL
+ *   (symmetric, zero point 8). MoE weights stack experts on the leading dimension.
+ */
+#ifndef W4A8_MI355X_H
+#define W4A8_MI355X_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define W4A8_OK 0
+#define W4A8_ERR_INVALID 1
+#define W4A8_ERR_UNSUPPORTED 2
+#define W4A8_ERR_HIP 3
+
+/* ABI revision (1). */
+int w4a8_abi_version(void);
+
+/* Message of the calling thread's last failed call. */
+const char* w4a8_last_error(void);
+
+/* Per-token fp8-e4m3 activation quant: s = max(amax/448, 1e-8), q = e4m3_rne(x/s).
+ * Replaces fp8_wmma's in-op compute_act_fp8_and_scales_kernel (python/minisgl/quant/kernels.py:
+ * 1512-1515, contract :1703-1712) and the (x_fp8, act_scales) pair tail_hip.rms_norm_quant emits
+ * (python/minisgl/layers/norm.py:27-46). row_count: optional device int32 bounding the rows done
+ * (rows at and past it are left untouched), for graph-captured MoE launches. */
+int w4a8_act_quant(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, uint8_t* x_fp8, int64_t ldq,
+                   float* act_scales, const int32_t* row_count, void* stream);
+
+/* Bytes of the W4 tile layout for an (N, K) weight (N % 16 == 0); -1 on bad sizes. */
+int64_t w4a8_tile_bytes(int64_t N, int64_t K);
+
+/* Load-time repack of op-layout codes (rows = N, or E*N for a stacked MoE weight) into W4 tiles.
+ * Replaces the layout half of awq_to_op_layout / gptq_to_op_layout (python/minisgl/quant/
+ * kernels.py:255-346) and mxfp4.convert_mxfp4_weight / convert_mxfp4_moe_e8m0
+ * (python/minisgl/quant/mxfp4.py:134-206), whose (N, K/8) int32 output is this call's input. */
+int w4a8_repack_weights(const int32_t* w_packed, int64_t N, int64_t K, int wfmt, void* w_tile, void* stream);
+
+/* Workspace bytes w4a8_gemm needs for (M, N, K) and a kernel choice (0 auto, 1 decode, 2 prefill). */
+int64_t w4a8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int kernel);
+
+/* Dense W4A8 GEMM: out[m, n] = act_scales[m] * sum_g scale[g, n] * sum_{k in g} e4m3(x[m,k]) * w(n,k).
+ * Replaces fp8_wmma.mmq_fp8_gemm (python/minisgl/quant/kernels.py:1686-1734; arms decode_gemv and
+ * wmma_tiled_tuned chosen by _pick_dense_kernel :1456-1632) and, with silu = 1,
+ * fp8_wmma.mmq_fp8_gemm_silu (kernels.py:1737-1753): N = 2*inter with gate rows first, output
+ * (M, inter) = silu(gate) * up rounded as in tools/w4a8_gemm_silu_parity.py:52-54.
+ * kernel: 0 auto (M <= 16 decode, else prefill), 1 decode, 2 prefill. */
+int w4a8_gemm(const uint8_t* x_fp8, int64_t ldx, const float* act_scales, int64_t M, const void* w_tile, int64_t N,
+              int64_t K, const void* scales, int scale_fmt, const int32_t* zeros, int wfmt, int64_t group_size,
+              void* out, int out_dtype, int64_t ldo, int silu, void* workspace, int64_t workspace_bytes, int kernel,
+              void* stream);
+
+/* Softmax + top-k (ties keep the lower expert index) + optional renormalisation. Replaces the
+ * route half of moe_hip.moe_route_align (python/minisgl/quant/kernels.py:423-447; tie rule
+ * python/minisgl/layers/moe.py:1218-1227). E <= 512. */
+int w4a8_moe_route(const void* logits, int logits_dtype, int64_t T, int64_t E, int top_k, int renormalize,
+                   float* topk_w, int32_t* topk_ids, void* stream);
+
+/* Padded capacity numel + (E+1)*(block_m-1) of sorted_ids (python/minisgl/moe/fused.py:94). */
+int64_t w4a8_moe_padded_capacity(int64_t numel, int64_t E, int block_m);
+
+/* moe_align_block_size: replaces moe_hip.moe_align and the align half of moe_route_align
+ * (python/minisgl/quant/kernels.py:686-695; contract python/minisgl/moe/fused.py:120-176).
+ * Writes sorted_ids (P), expert_ids (ceil(P/block_m)), ntp (1) and, if non-NULL, inv_pos (numel):
+ * the position of every slot in sorted_ids. Deterministic. */
+int w4a8_moe_align(const int32_t* topk_ids, int64_t numel, int64_t E, int block_m, int64_t P, int32_t* sorted_ids,
+                   int32_t* expert_ids, int32_t* ntp, int32_t* inv_pos, void* stream);
+
+/* Workspace bytes w4a8_moe_gemm needs. */
+int64_t w4a8_moe_gemm_workspace_bytes(int64_t numel, int64_t E, int block_m, int64_t P, int64_t N, int64_t K,
+                                      int kernel);
+
+/* Grouped W4A8 GEMM over align blocks. a_by_token = 1: row p reads A row sorted_ids[p]/top_k
+ * (gemm1, with silu = 1 the fused gate/up epilogue of fp8_wmma.mmq_fp8_moe_gemm1_silu[_flag],
+ * python/minisgl/quant/kernels.py:744-765); a_by_token = 0: row p reads A row p (gemm2,
+ * fp8_wmma.mmq_fp8_moe_gemm[_flag], kernels.py:851-874). Rows at or past *ntp and padding slots
+ * are skipped. kernel: 0 auto (block_m < 64 decode), 1 decode, 2 prefill (block_m % 64 == 0). */
+int w4a8_moe_gemm(const uint8_t* a_fp8, int64_t lda, const float* a_scales, int a_by_token, const int32_t* sorted_ids,
+                  const int32_t* expert_ids, const int32_t* ntp, int64_t numel, int top_k, int block_m, int64_t P,
+                  const void* w_tile, int64_t E, int64_t N, int64_t K, const void* scales, int scale_fmt,
+                  const int32_t* zeros, int wfmt, int64_t group_size, void* out, int out_dtype, int64_t ldo, int silu,
+                  void* workspace, int64_t workspace_bytes, int kernel, void* stream);
+
+/* Top-k weighted combine: out[t] = sum_j topk_w[t, j] * y[inv_pos[t*top_k + j]] in f32.
+ * Replaces fp8_wmma.mmq_fp8_moe_gather_reduce (python/minisgl/quant/kernels.py:876-882). */
+int w4a8_moe_combine(const float* y, int64_t ldy, const int32_t* inv_pos, const float* topk_w, int64_t T, int top_k,
+                     int64_t H, void* out, int out_dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* W4A8_MI355X_H */

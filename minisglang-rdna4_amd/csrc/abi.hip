@@ -1,0 +1,235 @@
+// extern "C" entry points of libw4a8_mi355x.so (declared in include/w4a8_mi355x.h).
+//
+// Every entry point validates its arguments on the host and returns a status code; the message of
+// the last failure on the calling thread is available from w4a8_last_error(). No entry point
+// allocates device memory: outputs and workspaces come from the caller.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "gemm_args.h"
+
+namespace w4a8 {
+int launch_act_quant(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx, uint8_t* q,
+                     int64_t ldq, float* scales, const int32_t* row_count, hipStream_t stream);
+int launch_repack(const int32_t* w, int64_t N, int64_t K, int wfmt, void* out, hipStream_t stream);
+int launch_gemv(GemmArgs p, int64_t row_blocks, hipStream_t stream);
+size_t gemv_workspace_bytes(int64_t M, int64_t N, int64_t K, int grouped, int64_t row_blocks);
+int launch_prefill(const GemmArgs& p, int64_t rows_to_cover, int bm_rows, hipStream_t stream);
+int launch_moe_route(const void* logits, int dtype, int64_t T, int E, int top_k, int renorm, float* tw,
+                     int32_t* ids, hipStream_t stream);
+int launch_moe_align(const int32_t* ids, int64_t numel, int E, int bm, int64_t P, int32_t* sorted_ids,
+                     int32_t* expert_ids, int32_t* ntp, int32_t* inv_pos, hipStream_t stream);
+int launch_moe_combine(const float* y, int64_t ldy, const int32_t* inv_pos, const float* tw, int64_t T,
+                       int top_k, int64_t H, void* out, int dtype, hipStream_t stream);
+}  // namespace w4a8
+
+using namespace w4a8;
+
+static thread_local char g_err[512];
+
+static int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+static int hip_status(int rc, const char* what) {
+  if (rc == kOk) return kOk;
+  hipError_t e = hipGetLastError();
+  return fail(kErrHip, "%s: HIP launch failed (%s)", what, hipGetErrorString(e));
+}
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+static const int kGemvMaxRows = 16;
+
+// Bound on align blocks that can hold routed rows: every expert with rows contributes
+// ceil(rows/bm) blocks, so at most numel/bm + min(E, numel) of them are non-empty.
+static int64_t moe_max_blocks(int64_t numel, int64_t E, int bm, int64_t P) {
+  int64_t bound = numel / bm + (E < numel ? E : numel);
+  int64_t cap = (P + bm - 1) / bm;
+  return bound < cap ? bound : cap;
+}
+
+static int check_weights(const char* who, int64_t N, int64_t K, int scale_fmt, const void* zeros, int wfmt,
+                         int64_t group) {
+  if (N <= 0 || K <= 0) return fail(kErrInvalid, "%s: N=%lld K=%lld must be positive", who, (long long)N, (long long)K);
+  if (N % 16) return fail(kErrInvalid, "%s: N=%lld must be a multiple of 16", who, (long long)N);
+  if (K % 32) return fail(kErrInvalid, "%s: K=%lld must be a multiple of 32", who, (long long)K);
+  if (wfmt != kInt4 && wfmt != kE2M1) return fail(kErrInvalid, "%s: unknown weight format %d", who, wfmt);
+  if (scale_fmt != kScaleF16 && scale_fmt != kScaleE8M0)
+    return fail(kErrInvalid, "%s: unknown scale format %d", who, scale_fmt);
+  if (!(group == 32 || group == 64 || (group >= 128 && group % 128 == 0)))
+    return fail(kErrUnsupported, "%s: group_size=%lld unsupported (32, 64 or a multiple of 128)", who, (long long)group);
+  if (K % group) return fail(kErrInvalid, "%s: K=%lld is not a multiple of group_size=%lld", who, (long long)K, (long long)group);
+  if (wfmt == kE2M1 && zeros) return fail(kErrInvalid, "%s: e2m1 weights are symmetric; w_zeros must be empty", who);
+  if (scale_fmt == kScaleE8M0 && wfmt != kE2M1)
+    return fail(kErrInvalid, "%s: E8M0 (uint8) scales are only defined for e2m1 weights", who);
+  if (scale_fmt == kScaleE8M0 && group != 32)
+    return fail(kErrInvalid, "%s: E8M0 scales are per 32-element block (group_size=32), got %lld", who, (long long)group);
+  return kOk;
+}
+
+extern "C" {
+
+int w4a8_abi_version(void) { return 1; }
+
+const char* w4a8_last_error(void) { return g_err; }
+
+int w4a8_act_quant(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, uint8_t* x_fp8, int64_t ldq,
+                   float* act_scales, const int32_t* row_count, void* stream) {
+  if (x_dtype != kBF16 && x_dtype != kF16) return fail(kErrInvalid, "act_quant: x must be bf16 or fp16");
+  if (M < 0 || K <= 0 || K % 8) return fail(kErrInvalid, "act_quant: K=%lld must be a positive multiple of 8", (long long)K);
+  if (ldx < K || ldx % 8 || ldq < K || ldq % 8)
+    return fail(kErrInvalid, "act_quant: row strides must be >= K and multiples of 8 (ldx=%lld ldq=%lld)",
+                (long long)ldx, (long long)ldq);
+  if (!aligned16(x) || !aligned16(x_fp8)) return fail(kErrInvalid, "act_quant: x and x_fp8 must be 16-byte aligned");
+  return hip_status(launch_act_quant(x, x_dtype, M, K, ldx, x_fp8, ldq, act_scales, row_count, (hipStream_t)stream),
+                    "act_quant");
+}
+
+int64_t w4a8_tile_bytes(int64_t N, int64_t K) {
+  if (N <= 0 || K <= 0 || N % 16) return -1;
+  return (N / 16) * ((K + 127) / 128) * 1024;
+}
+
+int w4a8_repack_weights(const int32_t* w_packed, int64_t N, int64_t K, int wfmt, void* w_tile, void* stream) {
+  if (N <= 0 || N % 16) return fail(kErrInvalid, "repack: rows=%lld must be a positive multiple of 16", (long long)N);
+  if (K <= 0 || K % 32) return fail(kErrInvalid, "repack: K=%lld must be a positive multiple of 32", (long long)K);
+  if (wfmt != kInt4 && wfmt != kE2M1) return fail(kErrInvalid, "repack: unknown weight format %d", wfmt);
+  if (!aligned16(w_tile)) return fail(kErrInvalid, "repack: output must be 16-byte aligned");
+  return hip_status(launch_repack(w_packed, N, K, wfmt, w_tile, (hipStream_t)stream), "repack");
+}
+
+int64_t w4a8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int kernel) {
+  if (kernel == 2 || (kernel == 0 && M > kGemvMaxRows)) return 0;
+  return (int64_t)gemv_workspace_bytes(M, N, K, 0, (M + 15) / 16);
+}
+
+int w4a8_gemm(const uint8_t* x_fp8, int64_t ldx, const float* act_scales, int64_t M, const void* w_tile, int64_t N,
+              int64_t K, const void* scales, int scale_fmt, const int32_t* zeros, int wfmt, int64_t group_size,
+              void* out, int out_dtype, int64_t ldo, int silu, void* workspace, int64_t workspace_bytes, int kernel,
+              void* stream) {
+  int rc = check_weights("w4a8_gemm", N, K, scale_fmt, zeros, wfmt, group_size);
+  if (rc) return rc;
+  if (M < 0) return fail(kErrInvalid, "w4a8_gemm: M=%lld", (long long)M);
+  if (M == 0) return kOk;
+  if (ldx < K || ldx % 16 || !aligned16(x_fp8))
+    return fail(kErrInvalid, "w4a8_gemm: x_fp8 rows must be 16-byte aligned with stride >= K (ldx=%lld)", (long long)ldx);
+  if (out_dtype != kBF16 && out_dtype != kF16 && out_dtype != kF32)
+    return fail(kErrInvalid, "w4a8_gemm: unknown output dtype %d", out_dtype);
+  if (silu && (N % 32)) return fail(kErrInvalid, "w4a8_gemm: fused silu needs N=2*inter with inter %% 16 == 0 (N=%lld)", (long long)N);
+  if (silu && out_dtype == kF32) return fail(kErrInvalid, "w4a8_gemm: fused silu rounds through bf16/fp16; f32 output unsupported");
+  const int64_t nout = silu ? N / 2 : N;
+  if (ldo < nout) return fail(kErrInvalid, "w4a8_gemm: ldo=%lld < output width %lld", (long long)ldo, (long long)nout);
+  if (!aligned16(w_tile)) return fail(kErrInvalid, "w4a8_gemm: weight tiles must be 16-byte aligned");
+  if (kernel < 0 || kernel > 2) return fail(kErrInvalid, "w4a8_gemm: kernel must be 0 (auto), 1 (decode) or 2 (prefill)");
+  const bool decode = kernel == 1 || (kernel == 0 && M <= kGemvMaxRows);
+
+  GemmArgs p = {};
+  p.xq = x_fp8; p.ldx = ldx; p.act_scales = act_scales; p.M = M;
+  p.N = N; p.K = K; p.KT = (K + 127) / 128;
+  p.wt = reinterpret_cast<const uint4*>(w_tile);
+  p.scales = scales; p.sfmt = scale_fmt; p.zeros = zeros; p.group = (int)group_size; p.wfmt = wfmt;
+  p.out = out; p.out_dtype = out_dtype; p.ldo = ldo; p.silu = silu;
+  p.top_k = 1; p.bm = 16;
+  if (decode) {
+    const int64_t rb = (M + 15) / 16;
+    const size_t need = gemv_workspace_bytes(M, N, K, 0, rb);
+    if (need > 0 && (workspace == nullptr || (size_t)workspace_bytes < need))
+      return fail(kErrInvalid, "w4a8_gemm: decode split-K needs a %zu-byte workspace, got %lld", need,
+                  (long long)workspace_bytes);
+    p.partial = reinterpret_cast<float*>(workspace);
+    return hip_status(launch_gemv(p, rb, (hipStream_t)stream), "w4a8_gemm(decode)");
+  }
+  return hip_status(launch_prefill(p, M, 128, (hipStream_t)stream), "w4a8_gemm(prefill)");
+}
+
+int w4a8_moe_route(const void* logits, int logits_dtype, int64_t T, int64_t E, int top_k, int renormalize,
+                   float* topk_w, int32_t* topk_ids, void* stream) {
+  if (logits_dtype != kBF16 && logits_dtype != kF16 && logits_dtype != kF32)
+    return fail(kErrInvalid, "moe_route: logits must be bf16, fp16 or f32");
+  if (E <= 0 || E > 512) return fail(kErrUnsupported, "moe_route: num_experts=%lld outside [1, 512]", (long long)E);
+  if (top_k <= 0 || top_k > E || top_k > 64) return fail(kErrInvalid, "moe_route: top_k=%d invalid for E=%lld", top_k, (long long)E);
+  return hip_status(launch_moe_route(logits, logits_dtype, T, (int)E, top_k, renormalize, topk_w, topk_ids,
+                                     (hipStream_t)stream), "moe_route");
+}
+
+int64_t w4a8_moe_padded_capacity(int64_t numel, int64_t E, int block_m) {
+  return numel + (E + 1) * (block_m - 1);
+}
+
+int w4a8_moe_align(const int32_t* topk_ids, int64_t numel, int64_t E, int block_m, int64_t P, int32_t* sorted_ids,
+                   int32_t* expert_ids, int32_t* ntp, int32_t* inv_pos, void* stream) {
+  if (E <= 0 || E > 512) return fail(kErrUnsupported, "moe_align: num_experts=%lld outside [1, 512]", (long long)E);
+  if (block_m <= 0 || block_m % 16) return fail(kErrInvalid, "moe_align: block_m=%d must be a positive multiple of 16", block_m);
+  if (P < numel + (E + 1) * (block_m - 1))
+    return fail(kErrInvalid, "moe_align: capacity P=%lld < numel + (E+1)*(block_m-1)", (long long)P);
+  if (numel > 0x7fffffff) return fail(kErrInvalid, "moe_align: too many slots");
+  return hip_status(launch_moe_align(topk_ids, numel, (int)E, block_m, P, sorted_ids, expert_ids, ntp, inv_pos,
+                                     (hipStream_t)stream), "moe_align");
+}
+
+int64_t w4a8_moe_gemm_workspace_bytes(int64_t numel, int64_t E, int block_m, int64_t P, int64_t N, int64_t K,
+                                      int kernel) {
+  const bool decode = kernel == 1 || (kernel == 0 && block_m < 64);
+  if (!decode) return 0;
+  const int64_t rb = moe_max_blocks(numel, E, block_m, P) * block_m / 16;
+  return (int64_t)gemv_workspace_bytes(P, N, K, 1, rb);
+}
+
+int w4a8_moe_gemm(const uint8_t* a_fp8, int64_t lda, const float* a_scales, int a_by_token, const int32_t* sorted_ids,
+                  const int32_t* expert_ids, const int32_t* ntp, int64_t numel, int top_k, int block_m, int64_t P,
+                  const void* w_tile, int64_t E, int64_t N, int64_t K, const void* scales, int scale_fmt,
+                  const int32_t* zeros, int wfmt, int64_t group_size, void* out, int out_dtype, int64_t ldo, int silu,
+                  void* workspace, int64_t workspace_bytes, int kernel, void* stream) {
+  int rc = check_weights("w4a8_moe_gemm", N, K, scale_fmt, zeros, wfmt, group_size);
+  if (rc) return rc;
+  if (E <= 0 || E > 512) return fail(kErrUnsupported, "w4a8_moe_gemm: num_experts=%lld outside [1, 512]", (long long)E);
+  if (block_m <= 0 || block_m % 16) return fail(kErrInvalid, "w4a8_moe_gemm: block_m=%d must be a multiple of 16", block_m);
+  if (lda < K || lda % 16 || !aligned16(a_fp8)) return fail(kErrInvalid, "w4a8_moe_gemm: A rows must be 16-byte aligned, stride >= K");
+  if (out_dtype != kBF16 && out_dtype != kF16 && out_dtype != kF32) return fail(kErrInvalid, "w4a8_moe_gemm: unknown output dtype");
+  if (silu && (N % 32 || out_dtype == kF32)) return fail(kErrInvalid, "w4a8_moe_gemm: fused silu needs N %% 32 == 0 and bf16/fp16 output");
+  const int64_t nout = silu ? N / 2 : N;
+  if (ldo < nout) return fail(kErrInvalid, "w4a8_moe_gemm: ldo=%lld < output width %lld", (long long)ldo, (long long)nout);
+  if (kernel < 0 || kernel > 2) return fail(kErrInvalid, "w4a8_moe_gemm: kernel must be 0, 1 or 2");
+  const bool decode = kernel == 1 || (kernel == 0 && block_m < 64);
+  if (!decode && block_m % 64) return fail(kErrInvalid, "w4a8_moe_gemm: the prefill arm needs block_m %% 64 == 0 (got %d)", block_m);
+  if (numel == 0) return kOk;
+
+  GemmArgs p = {};
+  p.xq = a_fp8; p.ldx = lda; p.act_scales = a_scales; p.M = P;
+  p.N = N; p.K = K; p.KT = (K + 127) / 128;
+  p.wt = reinterpret_cast<const uint4*>(w_tile);
+  p.scales = scales; p.sfmt = scale_fmt; p.zeros = zeros; p.group = (int)group_size; p.wfmt = wfmt;
+  p.sorted_ids = sorted_ids; p.expert_ids = expert_ids; p.ntp = ntp; p.top_k = top_k; p.num_slots = numel;
+  p.bm = block_m; p.a_by_token = a_by_token;
+  p.w_expert_tiles = (N / 16) * p.KT;
+  p.s_expert_stride = (K / group_size) * N;
+  p.z_expert_stride = (K / group_size) * (N / 8);
+  p.out = out; p.out_dtype = out_dtype; p.ldo = ldo; p.silu = silu;
+  const int64_t nblk = moe_max_blocks(numel, E, block_m, P);
+  if (decode) {
+    const int64_t rb = nblk * block_m / 16;
+    const size_t need = gemv_workspace_bytes(P, N, K, 1, rb);
+    if (need > 0 && (workspace == nullptr || (size_t)workspace_bytes < need))
+      return fail(kErrInvalid, "w4a8_moe_gemm: decode split-K needs a %zu-byte workspace, got %lld", need,
+                  (long long)workspace_bytes);
+    p.partial = reinterpret_cast<float*>(workspace);
+    return hip_status(launch_gemv(p, rb, (hipStream_t)stream), "w4a8_moe_gemm(decode)");
+  }
+  const int bm_rows = block_m % 128 == 0 ? 128 : 64;
+  return hip_status(launch_prefill(p, nblk * block_m, bm_rows, (hipStream_t)stream), "w4a8_moe_gemm(prefill)");
+}
+
+int w4a8_moe_combine(const float* y, int64_t ldy, const int32_t* inv_pos, const float* topk_w, int64_t T, int top_k,
+                     int64_t H, void* out, int out_dtype, void* stream) {
+  if (out_dtype != kBF16 && out_dtype != kF16 && out_dtype != kF32) return fail(kErrInvalid, "moe_combine: unknown dtype");
+  if (ldy < H) return fail(kErrInvalid, "moe_combine: ldy < H");
+  return hip_status(launch_moe_combine(y, ldy, inv_pos, topk_w, T, top_k, H, out, out_dtype, (hipStream_t)stream),
+                    "moe_combine");
+}
+
+}  // extern "C"

@@ -1,0 +1,45 @@
+// Argument block shared by the dense and grouped (MoE) W4A8 GEMM kernels.
+#pragma once
+#include "w4a8_common.h"
+
+namespace w4a8 {
+
+struct GemmArgs {
+  // activations: fp8 rows (row stride ldx bytes) + per-row f32 scale
+  const uint8_t* xq;
+  int64_t ldx;
+  const float* act_scales;
+  int64_t M;          // dense: rows of x/out. grouped: padded row capacity P
+  // weights
+  int64_t N;          // output channels of the weight (2*inter for the fused-silu arms)
+  int64_t K;
+  int64_t KT;         // tiles along K = ceil(K/128)
+  const uint4* wt;    // W4 tiles
+  const void* scales; // (K/g, N) group-major, fp16 or E8M0 uint8
+  int sfmt;
+  const int32_t* zeros;  // (K/g, N/8) packed or null (symmetric, zero = 8)
+  int group;
+  int wfmt;
+  // grouped rows (null sorted_ids => dense)
+  const int32_t* sorted_ids;
+  const int32_t* expert_ids;
+  const int32_t* ntp;
+  int top_k;
+  int64_t num_slots;  // T * top_k; sorted ids >= this are padding
+  int bm;             // align block size
+  int a_by_token;     // 1: A row = token = slot / top_k (gemm1); 0: A row = padded position (gemm2)
+  int64_t w_expert_tiles;  // tiles per expert
+  int64_t s_expert_stride; // scale elements per expert
+  int64_t z_expert_stride; // zero words per expert
+  // output
+  void* out;
+  int out_dtype;
+  int64_t ldo;        // elements
+  int silu;           // 1: out[:, j] = silu(y[:, j]) * y[:, j + N/2]
+  // split-K
+  float* partial;     // (SK, M, N) f32 when SK > 1
+  int SK;
+  int64_t kps;        // tiles per split
+};
+
+}  // namespace w4a8

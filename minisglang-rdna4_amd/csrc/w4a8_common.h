@@ -1,0 +1,150 @@
+// Shared definitions for the gfx950 (CDNA4) W4A8 kernels.
+//
+// MFMA operand layouts used throughout (v_mfma_scale_f32_16x16x128_f8f6f4, measured on MI355X):
+//   * fp8 operand (A activations, or B weights after int4 unpack): lane l, q = l >> 4, holds the
+//     32 bytes of row/column (l & 15) at K offsets [16q, 16q+16) in bytes 0..15 and
+//     [64+16q, 64+16q+16) in bytes 16..31 of its 8 VGPRs.
+//   * fp4 operand (B weights, MXFP4): lane l holds K offsets [32q, 32q+32) in 4 VGPRs, element
+//     32q+e in nibble (e & 1) of byte e/2 -- the checkpoint's own packing order.
+//   * E8M0 block scales: the scale of row/column i for K block b (32 wide) is read from lane i+16b.
+//   * C (16x16 f32): lane l holds rows 4q + r (r = 0..3) of column l & 15.
+//
+// Weight tile layout in HBM ("W4 tile"): a matrix of N output channels x K inputs is cut into
+// 16-channel x 128-K tiles of 1024 bytes, ordered [N/16][ceil(K/128)][64 lanes][16 bytes], so a
+// wave loads one tile as one coalesced 1 KB request and each lane receives exactly its MFMA
+// operand. Codes stay 4-bit.
+//   * int4: the 16 bytes of lane l are four dwords d; byte i of dword d holds operand element
+//     8d+i in its low nibble and 8d+4+i in its high nibble, where operand element e maps to K as
+//     in the fp8 layout above. The nibble is a sign-magnitude code of (q - 7.5):
+//     c = q >= 8 ? q - 8 : 15 - q, value = (c & 8 ? -1 : 1) * ((c & 7) + 0.5). One v_perm over an
+//     8-entry e4m3 table plus a sign OR turns it into fp8. The -0.5 shift is undone with the row
+//     sums R (sum_k x) that an extra MFMA against a constant 0.5 operand provides:
+//       sum_k x (q - z) = sum_k x v + (7.5 - z) * R.
+//   * e2m1: lane l's 16 bytes are the checkpoint's 4 words for K [32q, 32q+32), unchanged.
+// K is padded to a multiple of 128 with code 0 (activations there are zero).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace w4a8 {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int kTileN = 16;
+constexpr int kTileK = 128;
+constexpr int kTileBytes = 1024;
+
+// status codes shared with the C ABI
+constexpr int kOk = 0;
+constexpr int kErrInvalid = 1;
+constexpr int kErrUnsupported = 2;
+constexpr int kErrHip = 3;
+
+enum DType { kBF16 = 0, kF16 = 1, kF32 = 2 };
+enum ScaleFmt { kScaleF16 = 0, kScaleE8M0 = 1 };
+enum WFmt { kInt4 = 0, kE2M1 = 1 };
+
+// e4m3 constants
+constexpr uint32_t kE4M3Half4 = 0x30303030u;  // +0.5 in every byte
+
+// fp8 x fp8 MFMA, unit scales.
+__device__ __forceinline__ v4f mfma_f8f8(const v8i& a, const v8i& b, const v4f& c) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
+}
+// fp8 x fp8 with a per-lane B block scale (E8M0 byte in the low byte of sb).
+__device__ __forceinline__ v4f mfma_f8f8_sb(const v8i& a, const v8i& b, const v4f& c, int sb) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, sb);
+}
+// fp8 (A) x fp4 e2m1 (B) with a per-lane B block scale.
+__device__ __forceinline__ v4f mfma_f8f4_sb(const v8i& a, const v8i& b, const v4f& c, int sb) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 4, 0, 127, 0, sb);
+}
+
+// Sign-magnitude int4 code -> e4m3 bytes. LUT magnitudes (t + 0.5), t = 0..7:
+// 0.5 1.5 2.5 3.5 4.5 5.5 6.5 7.5 -> 30 3C 42 46 49 4B 4D 4F.
+__device__ __forceinline__ void unpack_sm4(uint32_t w, uint32_t& lo, uint32_t& hi) {
+  const uint32_t L0 = 0x46423C30u, L1 = 0x4F4D4B49u;
+  uint32_t t0 = __builtin_amdgcn_perm(L1, L0, w & 0x07070707u);
+  lo = ((w << 4) & 0x80808080u) | t0;
+  uint32_t t1 = __builtin_amdgcn_perm(L1, L0, (w >> 4) & 0x07070707u);
+  hi = (w & 0x80808080u) | t1;
+}
+
+// 16 stored bytes (uint4) -> 8-VGPR fp8 operand.
+__device__ __forceinline__ v8i unpack_tile_int4(const uint4& raw) {
+  v8i b;
+  uint32_t lo, hi;
+  unpack_sm4(raw.x, lo, hi); b[0] = (int)lo; b[1] = (int)hi;
+  unpack_sm4(raw.y, lo, hi); b[2] = (int)lo; b[3] = (int)hi;
+  unpack_sm4(raw.z, lo, hi); b[4] = (int)lo; b[5] = (int)hi;
+  unpack_sm4(raw.w, lo, hi); b[6] = (int)lo; b[7] = (int)hi;
+  return b;
+}
+
+__device__ __forceinline__ v8i fp4_operand(const uint4& raw) {
+  v8i b;
+  b[0] = (int)raw.x; b[1] = (int)raw.y; b[2] = (int)raw.z; b[3] = (int)raw.w;
+  b[4] = 0; b[5] = 0; b[6] = 0; b[7] = 0;
+  return b;
+}
+
+__device__ __forceinline__ v8i splat8(uint32_t v) {
+  v8i b;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) b[i] = (int)v;
+  return b;
+}
+
+// bf16 / fp16 scalar helpers (RNE)
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+__device__ __forceinline__ float f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+__device__ __forceinline__ uint16_t f32_to_f16(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+
+__device__ __forceinline__ float load_act(const uint16_t* p, int dtype) {
+  return dtype == kBF16 ? bf16_to_f32(*p) : f16_to_f32(*p);
+}
+__device__ __forceinline__ uint16_t to_dtype(float v, int dtype) {
+  return dtype == kBF16 ? f32_to_bf16(v) : f32_to_f16(v);
+}
+__device__ __forceinline__ float from_dtype(uint16_t h, int dtype) {
+  return dtype == kBF16 ? bf16_to_f32(h) : f16_to_f32(h);
+}
+
+// A operand: row pointer (already offset to the tile's K start), valid K extent in bytes from
+// the tile start (multiple of 16). Rows with a null pointer give zeros.
+__device__ __forceinline__ v8i load_a_operand(const uint8_t* row, int kvalid, int lane) {
+  v8i a;
+  const int q = lane >> 4;
+  uint4 lo = make_uint4(0, 0, 0, 0), hi = make_uint4(0, 0, 0, 0);
+  if (row) {
+    if (16 * q < kvalid) lo = *reinterpret_cast<const uint4*>(row + 16 * q);
+    if (64 + 16 * q < kvalid) hi = *reinterpret_cast<const uint4*>(row + 64 + 16 * q);
+  }
+  a[0] = (int)lo.x; a[1] = (int)lo.y; a[2] = (int)lo.z; a[3] = (int)lo.w;
+  a[4] = (int)hi.x; a[5] = (int)hi.y; a[6] = (int)hi.z; a[7] = (int)hi.w;
+  return a;
+}
+
+// Per-lane B scale that keeps only the K blocks of sub-group `sg` (of width 128/gpt) for
+// groups narrower than a tile: 127 (x1) for the lane's block inside the sub-group, 0 (x2^-127,
+// i.e. far below one f32 ulp of any accumulated value) outside it.
+__device__ __forceinline__ int subgroup_mask_scale(int lane, int gpt, int sg) {
+  const int blk = lane >> 4;           // K block (32 wide) the lane's scale governs
+  const int per = 4 / gpt;             // blocks per sub-group
+  return (blk / per == sg) ? 127 : 0;
+}
+
+__device__ __forceinline__ float load_scale(const void* scales, int fmt, int64_t idx) {
+  if (fmt == kScaleF16) return f16_to_f32(reinterpret_cast<const uint16_t*>(scales)[idx]);
+  uint32_t s = reinterpret_cast<const uint8_t*>(scales)[idx];
+  return s == 0 ? 5.877471754111438e-39f : __uint_as_float(s << 23);
+}
+
+}  // namespace w4a8

@@ -1,0 +1,563 @@
+"""W4A8 kernel provider: the reference's ``minisgl.quant.kernels`` operator API on MI355X kernels.
+
+Same names, argument meaning and refusal behaviour as python/minisgl/quant/kernels.py of the
+reference for the W4A8 path: ``awq_to_op_layout`` / ``gptq_to_op_layout`` (:255-346),
+``_moe_block_m`` (:355-420), ``_route_align`` (:423-447), ``_check_moe_scale_pair`` (:484-559),
+``w4a8_moe`` (:562-882), ``_pick_dense_kernel`` (:1456-1632), ``w4a8_linear`` (:1686-1734),
+``w4a8_linear_silu`` (:1737-1753). Underneath, every op calls libw4a8_mi355x.so through ctypes on
+the current torch stream; outputs and workspaces are allocated here with torch, never in C.
+
+Weights: the ops accept the reference's op layout (int32 ``(N, K/8)``, ``(E, N, K/8)`` for MoE) and
+also the W4 tile layout (uint8 ``(N/16, ceil(K/128), 1024)``, ``(E, N/16, ceil(K/128), 1024)``)
+that :func:`repack_w4` produces once at load. An op-layout weight is repacked on every call
+(correct, and visible in the dispatch ledger as ``+repack``); the load path
+(``method.W4A8LinearMethod``, the MoE containers) stores tiles so the serving call never repacks.
+"""
+from __future__ import annotations
+
+import os
+
+import torch
+
+from .. import _abi
+from .._hip_engage import engaged
+
+# AWQ "gemm" reverse pack order: undoes the [0,2,4,6,1,3,5,7] channel interleave of AWQ packing
+# (python/minisgl/quant/kernels.py:22).
+_REVERSE_AWQ_PACK_ORDER = [0, 4, 1, 5, 2, 6, 3, 7]
+
+# Decode band: the skinny-M kernel serves up to 16 rows (python/minisgl/quant/kernels.py:1663-1673
+# sets the same ceiling for both weight formats) and consumes K in 32-element fragments.
+_W4A8_GEMV_MAX_INT4 = 16
+_W4A8_GEMV_MAX_E2M1 = 16
+_W4A8_GEMV_K_MULTIPLE = 32
+
+# MoE gemm1 GEMV crossover and tile heights (python/minisgl/quant/kernels.py:130-131, 349-353).
+_MOE_GEMM1_GEMV_MAX = 32
+_MOE_WMMA_DIM = 16
+_MOE_BLOCK_M_CHOICES = (16, 32, 64, 128)
+
+
+# --------------------------------------------------------------------------------------------
+# layout conversion (load time)
+# --------------------------------------------------------------------------------------------
+def _pack_along_last(vals: torch.Tensor, bits: int) -> torch.Tensor:
+    """(..., L) small ints -> (..., L/pf) int32, element j of each group of pf in nibble j."""
+    pf = 32 // bits
+    mask = (1 << bits) - 1
+    *lead, L = vals.shape
+    v = (vals.to(torch.int64) & mask).reshape(*lead, L // pf, pf)
+    shifts = torch.arange(0, 32, bits, dtype=torch.int64, device=vals.device)
+    words = (v << shifts).sum(dim=-1)
+    return (words & 0xFFFFFFFF).to(torch.int32)
+
+
+def _unpack_along_last(words: torch.Tensor, bits: int) -> torch.Tensor:
+    """(..., W) int32 -> (..., W*pf) int32 nibbles, nibble j of a word first-to-last."""
+    pf = 32 // bits
+    mask = (1 << bits) - 1
+    shifts = torch.arange(0, 32, bits, dtype=torch.int32, device=words.device)
+    u = (words.unsqueeze(-1) >> shifts) & mask
+    return u.reshape(*words.shape[:-1], words.shape[-1] * pf)
+
+
+def awq_to_op_layout(
+    qweight: torch.Tensor,  # (K, N//pf) int32, AWQ-packed along the output dim, interleaved
+    scales: torch.Tensor,  # (K//group, N) fp16
+    qzeros: torch.Tensor | None,  # (K//group, N//pf) int32 AWQ-packed, or None (symmetric)
+    *,
+    bits: int = 4,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor | None]:
+    """One dense AWQ matrix -> op layout (w_packed (N, K/8) i32, scales (K/g, N) f16, zeros
+    (K/g, N/8) i32 | None). Restates python/minisgl/quant/kernels.py:255-299: undo the AWQ column
+    interleave, transpose to (N, K), repack 8 codes per int32 along K; zeros keep 8 channels per
+    int32 along N in natural order; scales stay group-major."""
+    assert bits == 4, "W4A8 path is 4-bit"
+    K, Np = qweight.shape
+    rev = torch.tensor(_REVERSE_AWQ_PACK_ORDER, dtype=torch.long, device=qweight.device)
+    u = _unpack_along_last(qweight, bits).reshape(K, Np, 8)[:, :, rev].reshape(K, Np * 8)  # (K, N)
+    w_packed = _pack_along_last(u.t().contiguous(), bits)  # (N, K/8)
+    scales_op = scales.contiguous().to(torch.float16)
+    zeros_op = None
+    if qzeros is not None:
+        G = qzeros.shape[0]
+        uz = _unpack_along_last(qzeros, bits).reshape(G, Np, 8)[:, :, rev].reshape(G, Np * 8)
+        zeros_op = _pack_along_last(uz, bits)
+    return w_packed, scales_op, zeros_op
+
+
+def gptq_to_op_layout(
+    qweight: torch.Tensor,  # (K//pf, N) int32, packed along K, natural nibble order
+    scales: torch.Tensor,  # (K//group, N) fp16
+    qzeros: torch.Tensor | None,  # (K//group, N//pf) int32; stored zero + 1 is the zero point
+    *,
+    bits: int = 4,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """One dense GPTQ matrix -> op layout. Restates python/minisgl/quant/kernels.py:302-346:
+    unpack along K to (K, N), transpose, repack along K; zeros unpacked along N with AutoGPTQ's +1
+    folded in (symmetric checkpoints store 7 -> zero 8), asserted to fit 4 bits."""
+    assert bits == 4, "W4A8 path is 4-bit"
+    assert qzeros is not None, "GPTQ always ships qzeros"
+    Kp, N = qweight.shape
+    K = Kp * 8
+    u = _unpack_along_last(qweight.t().contiguous(), bits)  # (N, K): word kp nibble j -> k = 8kp + j
+    w_packed = _pack_along_last(u, bits)
+    scales_op = scales.contiguous().to(torch.float16)
+    G = qzeros.shape[0]
+    uz = _unpack_along_last(qzeros, bits).reshape(G, N) + 1
+    assert int(uz.max()) <= 15, f"GPTQ zero+1 overflows 4b (max={int(uz.max())})"
+    zeros_op = _pack_along_last(uz, bits)
+    assert w_packed.shape == (N, K // 8)
+    return w_packed, scales_op, zeros_op
+
+
+def tile_shape(n: int, k: int) -> tuple[int, int, int]:
+    return (n // 16, (k + 127) // 128, 1024)
+
+
+def repack_w4(w_packed: torch.Tensor, weight_is_e2m1: bool = False) -> torch.Tensor:
+    """Op layout -> W4 tile layout on the weight's device (one HIP launch).
+
+    (N, K/8) int32 -> (N/16, ceil(K/128), 1024) uint8; (E, N, K/8) -> (E, N/16, ceil(K/128), 1024).
+    """
+    if w_packed.dtype != torch.int32 or w_packed.dim() not in (2, 3):
+        raise TypeError(f"repack_w4: expected an int32 (N, K/8) or (E, N, K/8) tensor, got "
+                        f"{w_packed.dtype} {tuple(w_packed.shape)}")
+    if not w_packed.is_cuda:
+        raise RuntimeError("repack_w4: the weight must be on the GPU (the repack is a HIP kernel)")
+    lead = w_packed.shape[:-2]
+    N, K = w_packed.shape[-2], w_packed.shape[-1] * 8
+    rows = N * (w_packed.shape[0] if w_packed.dim() == 3 else 1)
+    if N % 16:
+        raise ValueError(f"repack_w4: N={N} must be a multiple of 16")
+    out = torch.empty((*lead, *tile_shape(N, K)), dtype=torch.uint8, device=w_packed.device)
+    lib = _abi.load()
+    _abi.check(
+        lib.w4a8_repack_weights(_abi.ptr(w_packed.contiguous()), rows, K,
+                                _abi.W_E2M1 if weight_is_e2m1 else _abi.W_INT4, _abi.ptr(out),
+                                _abi.stream_of(w_packed)),
+        "repack_w4",
+    )
+    return out
+
+
+def _as_tiles(w: torch.Tensor, k: int, weight_is_e2m1: bool, expect_dim: int, what: str) -> torch.Tensor:
+    """Accept op layout (repacked now) or tiles; return tiles."""
+    if w.dtype == torch.uint8 and w.dim() == expect_dim + 1 and w.shape[-1] == 1024:
+        if w.shape[-2] != (k + 127) // 128:
+            raise ValueError(f"{what}: tile tensor {tuple(w.shape)} does not match K={k}")
+        return w
+    if w.dtype == torch.int32 and w.dim() == expect_dim:
+        if w.shape[-1] * 8 != k:
+            raise ValueError(f"{what}: w_packed {tuple(w.shape)} does not match K={k}")
+        return repack_w4(w, weight_is_e2m1)
+    raise TypeError(f"{what}: weight must be op-layout int32 {'(E, N, K/8)' if expect_dim == 3 else '(N, K/8)'} "
+                    f"or W4 tiles, got {w.dtype} {tuple(w.shape)}")
+
+
+def _n_of(w: torch.Tensor) -> int:
+    return w.shape[-3] * 16 if w.dtype == torch.uint8 else w.shape[-2]
+
+
+# --------------------------------------------------------------------------------------------
+# activation quant
+# --------------------------------------------------------------------------------------------
+def act_quant(x: torch.Tensor, row_count: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-token fp8-e4m3 quant: returns (x_fp8 (M, K) uint8 e4m3fn codes, act_scales (M,) f32),
+    the pair the reference's producer emits (python/minisgl/layers/norm.py:27-46) and its
+    in-op pre-kernel computes (python/minisgl/quant/kernels.py:1703-1712)."""
+    if x.dim() != 2 or x.dtype not in (torch.bfloat16, torch.float16):
+        raise TypeError(f"act_quant: x must be a 2-D bf16/fp16 tensor, got {x.dtype} {tuple(x.shape)}")
+    x = x.contiguous()
+    M, K = x.shape
+    q = torch.empty((M, K), dtype=torch.uint8, device=x.device)
+    s = torch.empty((M,), dtype=torch.float32, device=x.device)
+    lib = _abi.load()
+    _abi.check(lib.w4a8_act_quant(_abi.ptr(x), _abi.dtype_code(x.dtype), M, K, K, _abi.ptr(q), K, _abi.ptr(s),
+                                  _abi.ptr(row_count), _abi.stream_of(x)), "act_quant")
+    return q, s
+
+
+def _fp8_bytes(t: torch.Tensor) -> torch.Tensor:
+    return t.view(torch.uint8) if t.dtype == torch.float8_e4m3fn else t
+
+
+# --------------------------------------------------------------------------------------------
+# dense
+# --------------------------------------------------------------------------------------------
+_PREFILL_NAMES = ("wmma_tiled_tuned", "mfma_prefill")
+_IN_PROLOGUE_NAMES = ("prefill_wmma", "prefill_wmma_ashuffle")
+
+
+def _pick_dense_kernel(m: int, weight_is_e2m1: bool = False, group_size: int = 128,
+                       k: int | None = None, n: int | None = None) -> str:
+    """Per-M arm choice, same rule as python/minisgl/quant/kernels.py:1456-1632: the streaming
+    decode kernel for M <= 16 when K is a multiple of 32, the MFMA tiled GEMM otherwise.
+    ``MINISGL_FORCE_TILED_LINEARS=1`` forces the tiled arm at every M."""
+    if os.environ.get("MINISGL_FORCE_TILED_LINEARS") == "1":
+        return "wmma_tiled_tuned"
+    gemv_max = _W4A8_GEMV_MAX_E2M1 if weight_is_e2m1 else _W4A8_GEMV_MAX_INT4
+    if m <= gemv_max and (k is None or k % _W4A8_GEMV_K_MULTIPLE == 0):
+        return "decode_gemv"
+    return "wmma_tiled_tuned"
+
+
+def _scale_fmt(scales: torch.Tensor, weight_is_e2m1: bool, what: str) -> int:
+    if scales.dtype == torch.float16:
+        return _abi.SCALE_F16
+    if scales.dtype == torch.uint8:
+        if not weight_is_e2m1:
+            raise TypeError(f"{what}: uint8 (E8M0) scales are only valid for e2m1 weights")
+        return _abi.SCALE_E8M0
+    raise TypeError(f"{what}: scales must be fp16 (group scales) or uint8 (E8M0), got {scales.dtype}")
+
+
+def _check_producer_pair(x: torch.Tensor, x_fp8, act_scales, what: str):
+    M, K = x.shape
+    if (x_fp8 is None) != (act_scales is None):
+        raise RuntimeError(f"{what}: x_fp8 and act_scales must be supplied TOGETHER (got only "
+                           f"{'x_fp8' if x_fp8 is not None else 'act_scales'})")
+    if x_fp8 is None:
+        return None, None
+    xq = _fp8_bytes(x_fp8)
+    if xq.dtype != torch.uint8 or tuple(xq.shape) != (M, K) or not xq.is_contiguous():
+        raise RuntimeError(f"{what}: x_fp8 must be a contiguous (M, K)=({M}, {K}) uint8/float8_e4m3fn tensor, "
+                           f"got {x_fp8.dtype} {tuple(x_fp8.shape)}")
+    if act_scales.dtype != torch.float32 or tuple(act_scales.shape) != (M,):
+        raise RuntimeError(f"{what}: act_scales must be (M,)=({M},) float32, got {act_scales.dtype} "
+                           f"{tuple(act_scales.shape)}")
+    return xq, act_scales.contiguous()
+
+
+def _dense(x, w_packed, scales, w_zeros, group_size, weight_is_e2m1, x_fp8, act_scales, silu, arm):
+    what = "w4a8_linear_silu" if silu else "w4a8_linear"
+    if x.dim() != 2 or x.dtype not in (torch.bfloat16, torch.float16):
+        raise TypeError(f"{what}: x must be 2-D bf16/fp16, got {x.dtype} {tuple(x.shape)}")
+    M, K = x.shape
+    N = _n_of(w_packed)
+    G = K // group_size
+    if K % group_size or tuple(scales.shape) != (G, N):
+        raise AssertionError(f"{what}: scales must be GROUP-major (K//group, N)=({G}, {N}), got "
+                             f"{tuple(scales.shape)}")
+    sfmt = _scale_fmt(scales, weight_is_e2m1, what)
+    if weight_is_e2m1 and w_zeros is not None and w_zeros.numel() > 0:
+        raise AssertionError(f"{what}: e2m1 weights are symmetric; w_zeros must be None")
+    if w_zeros is not None and w_zeros.numel() == 0:
+        w_zeros = None
+    if w_zeros is not None and (w_zeros.dtype != torch.int32 or tuple(w_zeros.shape) != (G, N // 8)):
+        raise AssertionError(f"{what}: w_zeros must be (K//group, N/8)=({G}, {N // 8}) int32, got "
+                             f"{w_zeros.dtype} {tuple(w_zeros.shape)}")
+    xq, xs = _check_producer_pair(x, x_fp8, act_scales, what)
+    tiles = _as_tiles(w_packed, K, weight_is_e2m1, 2, what)
+    if xq is None:
+        xq, xs = act_quant(x)
+    nout = N // 2 if silu else N
+    out = torch.empty((M, nout), dtype=x.dtype, device=x.device)
+    lib = _abi.load()
+    ws_bytes = int(lib.w4a8_gemm_workspace_bytes(M, N, K, arm))
+    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=x.device) if ws_bytes > 0 else None
+    _abi.check(
+        lib.w4a8_gemm(_abi.ptr(xq), K, _abi.ptr(xs), M, _abi.ptr(tiles), N, K, _abi.ptr(scales.contiguous()), sfmt,
+                      _abi.ptr(w_zeros.contiguous() if w_zeros is not None else None),
+                      _abi.W_E2M1 if weight_is_e2m1 else _abi.W_INT4, group_size, _abi.ptr(out),
+                      _abi.dtype_code(x.dtype), nout, int(silu), _abi.ptr(ws), ws_bytes, arm,
+                      _abi.stream_of(x)),
+        what,
+    )
+    return out, tiles is not w_packed
+
+
+def w4a8_linear(
+    x: torch.Tensor,
+    w_packed: torch.Tensor,  # (N, K/8) int32 op layout, or W4 tiles
+    scales: torch.Tensor,  # (K/group, N) fp16 group-major, or uint8 E8M0 (e2m1 only)
+    w_zeros: torch.Tensor | None,  # (K/group, N/8) int32 (asymmetric) or None (zero point 8)
+    group_size: int,
+    kernel: str | None = None,
+    weight_is_e2m1: bool = False,
+    x_fp8: torch.Tensor | None = None,  # producer-quantized activations (M, K) e4m3 codes
+    act_scales: torch.Tensor | None = None,  # (M,) f32
+) -> torch.Tensor:
+    """Dense W4A8 GEMM (M, K) @ (N, K)^T -> (M, N) in x's dtype (python/minisgl/quant/
+    kernels.py:1686-1734). Supplying the producer pair skips the op's own act-quant launch and is
+    bit-identical to it. Names ``prefill_wmma``/``prefill_wmma_ashuffle`` are the reference's
+    in-prologue-quant arms and refuse a pre-quantized pair loudly, as there."""
+    N = _n_of(w_packed)
+    K = x.shape[-1]
+    if kernel is None:
+        kernel = _pick_dense_kernel(x.shape[0], weight_is_e2m1, group_size, k=K, n=N)
+    if kernel == "decode_gemv":
+        arm = _abi.KERNEL_DECODE
+    elif kernel in _PREFILL_NAMES or kernel in _IN_PROLOGUE_NAMES:
+        if kernel in _IN_PROLOGUE_NAMES and x_fp8 is not None:
+            raise RuntimeError(f"w4a8_linear: kernel={kernel} quantizes activations in-prologue and refuses a "
+                               f"pre-quantized (x_fp8, act_scales) pair")
+        arm = _abi.KERNEL_PREFILL
+    else:
+        raise ValueError(f"w4a8_linear: unknown kernel {kernel!r}")
+    out, repacked = _dense(x, w_packed, scales, w_zeros, group_size, weight_is_e2m1, x_fp8, act_scales, False, arm)
+    engaged(f"w4a8_mi355x.gemm({kernel}{'+e2m1' if weight_is_e2m1 else ''}"
+            f"{'+prequant' if x_fp8 is not None else ''}{'+repack' if repacked else ''})")
+    return out
+
+
+def w4a8_linear_silu(
+    x: torch.Tensor,
+    w_packed: torch.Tensor,  # (2*inter, K/8) int32 [gate|up] op layout, or W4 tiles
+    scales: torch.Tensor,
+    w_zeros: torch.Tensor | None,
+    group_size: int,
+    weight_is_e2m1: bool = False,
+) -> torch.Tensor:
+    """Fused decode gate_up GEMV + silu_and_mul -> (M, inter) (python/minisgl/quant/
+    kernels.py:1737-1753). Bit-exact to w4a8_linear(kernel="decode_gemv") followed by the
+    round-silu-round-multiply replica of tools/w4a8_gemm_silu_parity.py:52-54."""
+    if x.shape[0] > _W4A8_GEMV_MAX_INT4 or x.shape[1] % _W4A8_GEMV_K_MULTIPLE:
+        raise AssertionError(f"w4a8_linear_silu: decode-only (M<=16, K%32==0), got {tuple(x.shape)}")
+    out, repacked = _dense(x, w_packed, scales, w_zeros, group_size, weight_is_e2m1, None, None, True,
+                           _abi.KERNEL_DECODE)
+    engaged(f"w4a8_mi355x.gemm_silu({'e2m1' if weight_is_e2m1 else 'int4'}{'+repack' if repacked else ''})")
+    return out
+
+
+# --------------------------------------------------------------------------------------------
+# MoE
+# --------------------------------------------------------------------------------------------
+def _moe_block_m(num_tokens: int, num_experts: int, top_k: int, flag_gemm1: bool | None = None) -> int:
+    """Grouped-GEMM tile height from the workload (python/minisgl/quant/kernels.py:355-420): the
+    largest of 16/32/64/128 not above the mean rows per expert; past the gemm1 GEMV crossover
+    (M > 32) at least 64 when the fused-silu tiled arm can run. ``MINISGL_MOE_BLOCK_M`` forces it.
+    Here block_m < 64 selects the skinny-M grouped kernel, block_m % 64 == 0 the MFMA tiled one."""
+    forced = os.environ.get("MINISGL_MOE_BLOCK_M")
+    if forced:
+        bm = int(forced)
+        assert bm in _MOE_BLOCK_M_CHOICES, f"MINISGL_MOE_BLOCK_M must be one of {_MOE_BLOCK_M_CHOICES}"
+        return bm
+    rows_per_expert = (num_tokens * top_k) / max(num_experts, 1)
+    bm = _MOE_WMMA_DIM
+    for choice in _MOE_BLOCK_M_CHOICES:
+        if choice <= rows_per_expert:
+            bm = choice
+    if flag_gemm1 is None or num_tokens <= _MOE_GEMM1_GEMV_MAX:
+        return bm
+    if flag_gemm1:
+        return max(bm, 64)
+    wide = bm
+    for choice in _MOE_BLOCK_M_CHOICES:
+        if choice <= min(2 * rows_per_expert, 64):
+            wide = choice
+    return max(bm, wide)
+
+
+def _route_align(gating_output: torch.Tensor, top_k: int, renormalize: bool, num_experts: int,
+                 block_size: int):
+    """softmax + top-k + renormalize + align in one call (python/minisgl/quant/kernels.py:423-447).
+    Returns (topk_weights f32, topk_ids i32, sorted_ids, expert_ids, num_tokens_post_pad)."""
+    tw, ids = _moe_route(gating_output, top_k, renormalize, num_experts)
+    sorted_ids, expert_ids, ntp, _ = _moe_align(ids, num_experts, block_size)
+    return tw, ids, sorted_ids, expert_ids, ntp
+
+
+def _moe_route(gating_output: torch.Tensor, top_k: int, renormalize: bool, num_experts: int):
+    engaged("w4a8_mi355x.moe_route_align")
+    g = gating_output.contiguous()
+    if g.dim() != 2 or g.shape[1] != num_experts:
+        raise AssertionError(f"moe route: gating_output must be (M, E={num_experts}), got {tuple(g.shape)}")
+    T = g.shape[0]
+    tw = torch.empty((T, top_k), dtype=torch.float32, device=g.device)
+    ids = torch.empty((T, top_k), dtype=torch.int32, device=g.device)
+    lib = _abi.load()
+    _abi.check(lib.w4a8_moe_route(_abi.ptr(g), _abi.dtype_code(g.dtype), T, num_experts, top_k, int(bool(renormalize)),
+                                  _abi.ptr(tw), _abi.ptr(ids), _abi.stream_of(g)), "moe_route")
+    return tw, ids
+
+
+def _moe_align(topk_ids: torch.Tensor, num_experts: int, block_size: int):
+    ids = topk_ids.to(torch.int32).contiguous()
+    numel = ids.numel()
+    lib = _abi.load()
+    P = int(lib.w4a8_moe_padded_capacity(numel, num_experts, block_size))
+    dev = ids.device
+    sorted_ids = torch.empty((P,), dtype=torch.int32, device=dev)
+    expert_ids = torch.empty(((P + block_size - 1) // block_size,), dtype=torch.int32, device=dev)
+    ntp = torch.empty((1,), dtype=torch.int32, device=dev)
+    inv = torch.empty((max(numel, 1),), dtype=torch.int32, device=dev)
+    _abi.check(lib.w4a8_moe_align(_abi.ptr(ids), numel, num_experts, block_size, P, _abi.ptr(sorted_ids),
+                                  _abi.ptr(expert_ids), _abi.ptr(ntp), _abi.ptr(inv), _abi.stream_of(ids)),
+               "moe_align")
+    return sorted_ids, expert_ids, ntp, inv
+
+
+def moe_align(topk_ids: torch.Tensor, num_experts: int, block_size: int):
+    """moe_align_block_size (python/minisgl/moe/fused.py:120-176) -> (sorted_ids, expert_ids, ntp)."""
+    engaged("w4a8_mi355x.moe_align")
+    s, e, n, _ = _moe_align(topk_ids, num_experts, block_size)
+    return s, e, n
+
+
+def _check_moe_scale_pair(w: torch.Tensor, scales: torch.Tensor, zeros: "torch.Tensor | None", which: str) -> None:
+    """The (scales dtype, zeros slot) pair must be one the grouped kernel dispatches
+    (python/minisgl/quant/kernels.py:484-559): fp16 folded scales with optional (E, G, N/8) AWQ
+    zeros; uint8 without zeros is MXFP4 E8M0. The NVFP4 two-level form (e4m3/uint8 block scale
+    with an (E, N) f32-as-int32 global) is recognised and validated exactly as there, and then
+    refused by w4a8_moe as outside this build."""
+    if scales.dtype == torch.float16:
+        if zeros is not None and zeros.dim() != 3:
+            raise AssertionError(
+                f"w4a8_moe {which}: fp16 (folded) scales pair with AWQ packed zeros (E, G, N/8) int32, but got a "
+                f"{zeros.dim()}-D {zeros.dtype} tensor {tuple(zeros.shape)}. A 2-D zeros tensor here is an NVFP4 "
+                f"per-output-channel global handed to the fp16 policy, which would stride it as if it were (E, G, N/8)."
+            )
+        return
+    if scales.dtype not in (torch.float8_e4m3fn, torch.uint8):
+        raise AssertionError(
+            f"w4a8_moe {which}: scales must be fp16 (folded per-group), float8_e4m3fn/uint8 (NVFP4 two-level block "
+            f"scale) or uint8 with no zeros (MXFP4 E8M0); got {scales.dtype}"
+        )
+    E, N = w.shape[0], _n_of(w)
+    if scales.dtype == torch.uint8 and zeros is None:
+        return
+    if zeros is None:
+        raise AssertionError(
+            f"w4a8_moe {which}: e4m3 block scales REQUIRE the per-output-channel f32 global in the zeros slot -- "
+            f"the two-level scale is incomplete without it."
+        )
+    if zeros.dtype != torch.int32 or tuple(zeros.shape) != (E, N):
+        raise AssertionError(
+            f"w4a8_moe {which}: the NVFP4 global must be the (E, N)=({E}, {N}) f32 vector BITCAST to int32; got "
+            f"{zeros.dtype} {tuple(zeros.shape)}. A `.to(torch.int32)` instead of `.view(torch.int32)` truncates "
+            f"every global to 0."
+        )
+
+
+def _moe_gemm(a, lda, a_scales, a_by_token, sorted_ids, expert_ids, ntp, numel, top_k, bm, P, tiles, E, N, K,
+              scales, sfmt, zeros, wfmt, group, out, out_dtype, ldo, silu, arm, what):
+    lib = _abi.load()
+    ws_bytes = int(lib.w4a8_moe_gemm_workspace_bytes(numel, E, bm, P, N, K, arm))
+    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=a.device) if ws_bytes > 0 else None
+    _abi.check(
+        lib.w4a8_moe_gemm(_abi.ptr(a), lda, _abi.ptr(a_scales), a_by_token, _abi.ptr(sorted_ids), _abi.ptr(expert_ids),
+                          _abi.ptr(ntp), numel, top_k, bm, P, _abi.ptr(tiles), E, N, K, _abi.ptr(scales), sfmt,
+                          _abi.ptr(zeros), wfmt, group, _abi.ptr(out), out_dtype, ldo, int(silu), _abi.ptr(ws),
+                          ws_bytes, arm, _abi.stream_of(a)),
+        what,
+    )
+
+
+def w4a8_moe(
+    x: torch.Tensor,  # (M, K) activations
+    w13: torch.Tensor,  # (E, 2*inter, K//8) i32 op layout (gate | up), or W4 tiles
+    w13_scales: torch.Tensor,  # (E, K//g, 2*inter) group-major fp16, or uint8 E8M0 (e2m1)
+    w13_zeros: torch.Tensor | None,  # (E, K//g, 2*inter/8) i32 AWQ zeros | None
+    w2: torch.Tensor,  # (E, K, inter//8) i32 op layout, or W4 tiles
+    w2_scales: torch.Tensor,  # (E, inter//g, K)
+    w2_zeros: torch.Tensor | None,
+    gating_output: torch.Tensor | None,  # (M, E); ignored when topk_ids/topk_weights are given
+    top_k: int,
+    renormalize: bool,
+    *,
+    topk_weights: torch.Tensor | None = None,
+    topk_ids: torch.Tensor | None = None,
+    kernel: str = "wmma",
+    block_m: int | None = None,
+    weight_is_e2m1: bool = False,
+    activation: str = "silu",
+    x_fp8: torch.Tensor | None = None,
+    act_scales: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Grouped W4A8 MoE forward (python/minisgl/quant/kernels.py:562-882): route -> align ->
+    gemm1 with fused silu(gate)*up (output in x's dtype) -> per-row act-quant of that buffer ->
+    gemm2 -> top-k weighted combine in f32 -> x's dtype. Returns (M, K)."""
+    return _moe_forward(x, w13, w13_scales, w13_zeros, w2, w2_scales, w2_zeros, gating_output, top_k, renormalize,
+                        topk_weights=topk_weights, topk_ids=topk_ids, block_m=block_m, weight_is_e2m1=weight_is_e2m1,
+                        activation=activation, x_fp8=x_fp8, act_scales=act_scales)["out"]
+
+
+def _moe_forward(x, w13, w13_scales, w13_zeros, w2, w2_scales, w2_zeros, gating_output, top_k, renormalize, *,
+                 topk_weights=None, topk_ids=None, block_m=None, weight_is_e2m1=False, activation="silu",
+                 x_fp8=None, act_scales=None) -> dict:
+    """w4a8_moe's pipeline; returns the output and every intermediate (route, align, the (P, inter)
+    gemm1 buffer) so each stage can be checked on its own."""
+    M, K = x.shape
+    E = w13.shape[0]
+    _grp = (K // w13_scales.shape[1]) if w13_scales.dim() == 3 else -1
+    assert _grp in (16, 32, 64, 128), (
+        f"w4a8_moe: derived group_size={_grp} from K={K} and G={w13_scales.shape[1]}; scales must be GROUP-major "
+        f"(E, K//group, N), got {tuple(w13_scales.shape)}"
+    )
+    _check_moe_scale_pair(w13, w13_scales, w13_zeros, "w13")
+    _check_moe_scale_pair(w2, w2_scales, w2_zeros, "w2")
+    for s, z in ((w13_scales, w13_zeros), (w2_scales, w2_zeros)):
+        if s.dtype == torch.float8_e4m3fn or (s.dtype == torch.uint8 and z is not None):
+            raise NotImplementedError("w4a8_moe: NVFP4 two-level scales are outside this build (W4A8 int4 and "
+                                      "MXFP4 E8M0 only)")
+    assert activation in ("silu", "gelu"), (
+        f"w4a8_moe supports activation 'silu' or 'gelu' (gelu_pytorch_tanh); got {activation!r}")
+    if activation != "silu":
+        raise NotImplementedError("w4a8_moe: only the fused silu epilogue is built for MI355X")
+    if x.dtype not in (torch.bfloat16, torch.float16):
+        raise TypeError(f"w4a8_moe: x must be bf16/fp16, got {x.dtype}")
+    N1 = _n_of(w13)
+    inter = N1 // 2
+    H2 = _n_of(w2)
+    if H2 != K:
+        raise AssertionError(f"w4a8_moe: w2 has {H2} output channels, expected hidden size {K}")
+    _grp2 = inter // w2_scales.shape[1]
+    if block_m is None:
+        block_m = _moe_block_m(M, E, top_k, flag_gemm1=True)
+
+    if topk_ids is None:
+        topk_weights, topk_ids = _moe_route(gating_output, top_k, renormalize, E)
+    else:
+        assert topk_weights is not None, "topk_weights required when topk_ids is given"
+        topk_weights = topk_weights.to(torch.float32).contiguous()
+        topk_ids = topk_ids.to(torch.int32).contiguous()
+        engaged("w4a8_mi355x.moe_align")
+    # the align's inverse positions (slot -> padded row) feed the combine
+    sorted_ids, expert_ids, ntp, inv = _moe_align(topk_ids, E, block_m)
+    P = sorted_ids.shape[0]
+    numel = topk_ids.numel()
+
+    if x_fp8 is not None:
+        assert act_scales is not None, "w4a8_moe: x_fp8 and act_scales must be supplied together"
+        assert tuple(x_fp8.shape) == (M, K) and tuple(act_scales.shape) == (M,), (
+            f"w4a8_moe: producer pair must be (M,K)=({M},{K}) and (M,)=({M},); got {tuple(x_fp8.shape)} and "
+            f"{tuple(act_scales.shape)}")
+        xq, xs = _fp8_bytes(x_fp8).contiguous(), act_scales.to(torch.float32).contiguous()
+    elif act_scales is not None:
+        raise AssertionError("w4a8_moe: act_scales given without x_fp8")
+    else:
+        xq, xs = act_quant(x)
+
+    wfmt = _abi.W_E2M1 if weight_is_e2m1 else _abi.W_INT4
+    t13 = _as_tiles(w13, K, weight_is_e2m1, 3, "w4a8_moe w13")
+    t2 = _as_tiles(w2, inter, weight_is_e2m1, 3, "w4a8_moe w2")
+    s13f = _scale_fmt(w13_scales, weight_is_e2m1, "w4a8_moe w13")
+    s2f = _scale_fmt(w2_scales, weight_is_e2m1, "w4a8_moe w2")
+    arm = _abi.KERNEL_DECODE if block_m < 64 else _abi.KERNEL_PREFILL
+    arm_name = "gemv" if arm == _abi.KERNEL_DECODE else "mfma"
+    e2 = "+e2m1" if weight_is_e2m1 else ""
+
+    buf2 = torch.empty((P, inter), dtype=x.dtype, device=x.device)
+    engaged(f"w4a8_mi355x.moe_gemm1_silu({arm_name}{e2}{'+prequant' if x_fp8 is not None else ''})")
+    _moe_gemm(xq, K, xs, 1, sorted_ids, expert_ids, ntp, numel, top_k, block_m, P, t13, E, N1, K,
+              w13_scales.contiguous(), s13f, w13_zeros.contiguous() if w13_zeros is not None else None, wfmt, _grp,
+              buf2, _abi.dtype_code(x.dtype), inter, True, arm, "w4a8_moe gemm1")
+
+    # gemm2 input: per-row fp8 re-quant of the (P, inter) buffer, rows bounded by ntp on device
+    q2 = torch.empty((P, inter), dtype=torch.uint8, device=x.device)
+    s2 = torch.empty((P,), dtype=torch.float32, device=x.device)
+    lib = _abi.load()
+    _abi.check(lib.w4a8_act_quant(_abi.ptr(buf2), _abi.dtype_code(x.dtype), P, inter, inter, _abi.ptr(q2), inter,
+                                  _abi.ptr(s2), _abi.ptr(ntp), _abi.stream_of(x)), "w4a8_moe act_quant(gemm2)")
+    y2 = torch.empty((P, K), dtype=torch.float32, device=x.device)
+    engaged(f"w4a8_mi355x.moe_gemm2({arm_name}{e2})")
+    _moe_gemm(q2, inter, s2, 0, sorted_ids, expert_ids, ntp, numel, top_k, block_m, P, t2, E, K, inter,
+              w2_scales.contiguous(), s2f, w2_zeros.contiguous() if w2_zeros is not None else None, wfmt, _grp2,
+              y2, _abi.F32, K, False, arm, "w4a8_moe gemm2")
+    out = torch.empty((M, K), dtype=x.dtype, device=x.device)
+    engaged("w4a8_mi355x.moe_combine")
+    _abi.check(lib.w4a8_moe_combine(_abi.ptr(y2), K, _abi.ptr(inv), _abi.ptr(topk_weights), M, top_k, K,
+                                    _abi.ptr(out), _abi.dtype_code(x.dtype), _abi.stream_of(x)), "w4a8_moe combine")
+    return {"out": out, "buf2": buf2, "y2": y2, "topk_weights": topk_weights, "topk_ids": topk_ids,
+            "sorted_ids": sorted_ids, "expert_ids": expert_ids, "ntp": ntp, "inv_pos": inv, "block_m": block_m}

@@ -1,0 +1,142 @@
+"""C ABI surface and host-side refusal behaviour -- no kernel launches, runs without a GPU."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from conftest import REPO, pkg
+
+HEADER = REPO / "include" / "w4a8_mi355x.h"
+
+
+def _declared() -> list[str]:
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^[A-Za-z_][\w\s\*]*?\b(w4a8_\w+)\s*\(", text, re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    abi = pkg("_abi")
+    if not abi.lib_path().exists():
+        pkg().__class__  # noqa: B018
+        import importlib.util
+
+        spec = importlib.util.spec_from_file_location("w4a8_build", REPO / "minisglang-rdna4_amd" / "build.py")
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        mod.build()
+    return abi.load()
+
+
+def test_header_declares_the_bound_surface():
+    abi = pkg("_abi")
+    assert _declared() == sorted(abi.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    raw = ctypes.CDLL(str(pkg("_abi").lib_path()))
+    for name in _declared():
+        assert hasattr(raw, name), f"{name} declared in {HEADER.name} but not exported"
+    assert lib.w4a8_abi_version() == 1
+
+
+def test_host_validation_rejects_before_launch(lib):
+    # N not a multiple of 16: refused on the host with a message, no device pointer touched
+    rc = lib.w4a8_gemm(None, 128, None, 1, None, 24, 128, None, 0, None, 0, 128, None, 0, 24, 0, None, 0, 0, None)
+    assert rc == 1 and b"multiple of 16" in lib.w4a8_last_error()
+    rc = lib.w4a8_gemm(None, 128, None, 1, None, 32, 128, None, 1, None, 0, 32, None, 0, 32, 0, None, 0, 0, None)
+    assert rc == 1 and b"E8M0" in lib.w4a8_last_error()
+    rc = lib.w4a8_gemm(None, 256, None, 1, None, 32, 256, None, 0, None, 0, 48, None, 0, 32, 0, None, 0, 0, None)
+    assert rc == 2 and b"group_size" in lib.w4a8_last_error()
+    rc = lib.w4a8_moe_align(None, 8, 600, 16, 10000, None, None, None, None, None)
+    assert rc == 2 and b"num_experts" in lib.w4a8_last_error()
+    rc = lib.w4a8_moe_align(None, 8, 8, 16, 10, None, None, None, None, None)
+    assert rc == 1 and b"capacity" in lib.w4a8_last_error()
+    assert lib.w4a8_tile_bytes(32, 256) == 2 * 2 * 1024
+    assert lib.w4a8_tile_bytes(32, 160) == 2 * 2 * 1024
+    assert lib.w4a8_moe_padded_capacity(8, 128, 16) == 8 + 129 * 15
+
+
+# ------------------------------------------------------------------------ provider refusals
+def _dense_args(M=4, K=256, N=64, g=128):
+    x = torch.randn(M, K).to(torch.bfloat16)
+    w = torch.zeros((N, K // 8), dtype=torch.int32)
+    s = torch.ones((K // g, N), dtype=torch.float16)
+    return x, w, s
+
+
+def test_half_producer_pair_refused_loudly():
+    K_ = pkg("quant.kernels")
+    x, w, s = _dense_args()
+    q = torch.zeros(x.shape, dtype=torch.uint8)
+    sc = torch.ones(x.shape[0])
+    with pytest.raises(RuntimeError, match="TOGETHER"):
+        K_.w4a8_linear(x, w, s, None, 128, x_fp8=q)
+    with pytest.raises(RuntimeError, match="TOGETHER"):
+        K_.w4a8_linear(x, w, s, None, 128, act_scales=sc)
+    with pytest.raises(RuntimeError, match="x_fp8 must be"):
+        K_.w4a8_linear(x, w, s, None, 128, x_fp8=q[:, :128].contiguous(), act_scales=sc)
+    with pytest.raises(RuntimeError, match="in-prologue"):
+        K_.w4a8_linear(x, w, s, None, 128, kernel="prefill_wmma", x_fp8=q, act_scales=sc)
+
+
+def test_scale_layout_and_format_refusals():
+    K_ = pkg("quant.kernels")
+    x, w, s = _dense_args()
+    with pytest.raises(AssertionError, match="GROUP-major"):
+        K_.w4a8_linear(x, w, s.t().contiguous(), None, 128)
+    with pytest.raises(TypeError, match="E8M0"):
+        K_.w4a8_linear(x, w, torch.zeros((256 // 32, 64), dtype=torch.uint8), None, 32)
+    with pytest.raises(AssertionError, match="symmetric"):
+        K_.w4a8_linear(x, w, torch.zeros((8, 64), dtype=torch.uint8), torch.zeros((8, 8), dtype=torch.int32), 32,
+                       weight_is_e2m1=True)
+
+
+# tests/mxfp4_moe_scale_guard_test.py:27-58 restated against this provider
+E, N, K, G = 4, 64, 256, 32
+
+
+def _w():
+    return torch.zeros((E, N, K // 8), dtype=torch.int32)
+
+
+def test_moe_scale_guard_accepts_mxfp4_e8m0():
+    pkg("quant.kernels")._check_moe_scale_pair(_w(), torch.zeros((E, K // G, N), dtype=torch.uint8), None, "w13")
+
+
+def test_moe_scale_guard_refuses_e4m3_without_global():
+    with pytest.raises(AssertionError, match="REQUIRE the per-output-channel f32 global"):
+        pkg("quant.kernels")._check_moe_scale_pair(
+            _w(), torch.zeros((E, K // 16, N), dtype=torch.float8_e4m3fn), None, "w13")
+
+
+def test_moe_scale_guard_validates_global():
+    chk = pkg("quant.kernels")._check_moe_scale_pair
+    chk(_w(), torch.zeros((E, K // 16, N), dtype=torch.uint8), torch.zeros((E, N), dtype=torch.int32), "w13")
+    with pytest.raises(AssertionError):
+        chk(_w(), torch.zeros((E, K // 16, N), dtype=torch.uint8), torch.zeros((E, N), dtype=torch.float32), "w13")
+
+
+def test_moe_scale_guard_fp16_and_unknown():
+    chk = pkg("quant.kernels")._check_moe_scale_pair
+    chk(_w(), torch.zeros((E, K // G, N), dtype=torch.float16), None, "w13")
+    with pytest.raises(AssertionError, match="scales must be"):
+        chk(_w(), torch.zeros((E, K // G, N), dtype=torch.bfloat16), None, "w13")
+    with pytest.raises(AssertionError, match="2-D zeros"):
+        chk(_w(), torch.zeros((E, K // G, N), dtype=torch.float16), torch.zeros((E, N), dtype=torch.int32), "w13")
+
+
+def test_moe_block_m_policy():
+    bm = pkg("quant.kernels")._moe_block_m
+    # BASELINE MoE config: E=128, top-8
+    assert [bm(T, 128, 8, flag_gemm1=True) for T in (1, 16, 256, 4096)] == [16, 16, 64, 128]
+    assert bm(64, 32, 4) == 16 and bm(2048, 32, 4) == 128
+
+
+def test_pick_dense_kernel():
+    pick = pkg("quant.kernels")._pick_dense_kernel
+    assert pick(1, k=4096) == "decode_gemv" and pick(16, k=4096) == "decode_gemv"
+    assert pick(17, k=4096) == "wmma_tiled_tuned" and pick(8, k=4100) == "wmma_tiled_tuned"
+    assert pick(16, weight_is_e2m1=True, group_size=32, k=8192) == "decode_gemv"

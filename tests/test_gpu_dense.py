@@ -1,0 +1,289 @@
+"""GPU parity of the dense W4A8 path against the CPU oracle (all through the C ABI).
+
+Bars: fp8 activation codes and scales bit-exact; GEMM outputs within 2e-3 relative L2 of the
+oracle's f64 result, with an element-wise structural guard (see assert_close_to_oracle). Full BASELINE sizes are checked against the oracle where it finishes in
+seconds (every decode shape), and through row subsets plus bit-exact row-split invariance for the
+prefill shapes.
+"""
+import numpy as np
+import pytest
+import torch
+
+import synth
+from conftest import pkg
+
+pytestmark = pytest.mark.gpu
+
+REL_L2 = 2e-3
+
+
+def _sync():
+    torch.cuda.synchronize()
+
+
+def assert_close_to_oracle(got: torch.Tensor, ref: np.ndarray, what: str):
+    """Contract bar: rel L2 <= 2e-3 against the f64 oracle. Structural guard: every element within
+    two output-dtype ulps plus 1e-4 of the output's magnitude (the MFMA's fp8 dot product
+    accumulates with slightly less than f32 precision, ~1e-5 relative, which shows up only where
+    outputs are small through cancellation)."""
+    g = got.float().cpu().numpy().astype(np.float64)
+    rel = np.linalg.norm(g - ref) / max(np.linalg.norm(ref), 1e-30)
+    dt = torch.bfloat16 if got.dtype == torch.bfloat16 else torch.float16
+    rounded = torch.from_numpy(ref).to(dt).double().numpy()
+    rel_r = np.linalg.norm(g - rounded) / max(np.linalg.norm(ref), 1e-30)
+    ulp_bits = 7 if got.dtype == torch.bfloat16 else 10
+    tol = 2 * np.abs(ref) * 2.0 ** -ulp_bits + 1e-4 * np.abs(ref).max()
+    bad = np.abs(g - ref) > tol
+    print(f"[parity] {what}: rel L2 {rel:.3e} (vs dtype-rounded oracle {rel_r:.3e}), outliers {int(bad.sum())}",
+          flush=True)
+    assert rel <= REL_L2, f"{what}: rel L2 {rel:.3e} > {REL_L2}"
+    assert not bad.any(), f"{what}: {bad.sum()} elements off, worst {np.abs(g - ref)[bad].max():.3e}"
+    return rel
+
+
+# ------------------------------------------------------------------------------- act quant
+@pytest.mark.parametrize("dtype,code", [(torch.bfloat16, 0), (torch.float16, 1)])
+@pytest.mark.parametrize("M,K", [(1, 4096), (16, 2560), (7, 14336), (33, 768), (5, 28672)])
+def test_act_quant_bit_exact(kernels, oracle, dev, dtype, code, M, K):
+    x = synth.activations(M, K, seed=M * 31 + K, outliers=True, dtype=dtype)
+    x[0, :] = 0  # scale floor row
+    if M > 2:
+        x[1, :] = 448.0
+        x[2, :] = (torch.linspace(-1e-3, 1e-3, K)).to(dtype)
+    q, s = kernels.act_quant(x.to(dev))
+    _sync()
+    rq, rs = oracle.act_quant(synth.bits16(x), code)
+    assert np.array_equal(s.cpu().numpy(), rs), "act scales differ"
+    assert np.array_equal(q.cpu().numpy(), rq), f"fp8 codes differ in {(q.cpu().numpy() != rq).sum()} places"
+
+
+# ------------------------------------------------------------------------------- repack
+@pytest.mark.parametrize("e2m1", [False, True])
+@pytest.mark.parametrize("N,K", [(32, 256), (48, 160), (16, 2560)])
+def test_repack_matches_tile_layout(kernels, dev, e2m1, N, K):
+    from test_layout import tile_reference
+
+    w = synth.pack_rows(torch.randint(0, 16, (N, K), generator=synth.gen(N + K), dtype=torch.int32))
+    t = kernels.repack_w4(w.to(dev), weight_is_e2m1=e2m1)
+    _sync()
+    assert tuple(t.shape) == (N // 16, (K + 127) // 128, 1024)
+    assert np.array_equal(t.cpu().numpy(), tile_reference(w.numpy(), K, e2m1))
+
+
+# ------------------------------------------------------------------------------- decode GEMV
+def _oracle_dense(oracle, x, w, s, z, g, e2m1=False):
+    xq, xs = oracle.act_quant(synth.bits16(x), 0 if x.dtype == torch.bfloat16 else 1)
+    return oracle.gemm(xq, xs, w.numpy(), s.numpy(), None if z is None else z.numpy(), g, e2m1)
+
+
+def test_config1_awq_asym_m16(kernels, oracle, dev):
+    """M=16, K=2560, N=9728, AWQ asym int4 g128, scales |N(0,.02)|+1e-4."""
+    M, K, N, g = 16, 2560, 9728, 128
+    x = synth.activations(M, K, seed=101)
+    w, s, z = synth.int4_weight(N, K, g, seed=102, asym=True, scale_floor=1e-4)
+    ref = _oracle_dense(oracle, x, w, s, z, g)
+    tiles = kernels.repack_w4(w.to(dev))
+    out = kernels.w4a8_linear(x.to(dev), tiles, s.to(dev), z.to(dev), g)
+    _sync()
+    assert out.dtype == torch.bfloat16 and tuple(out.shape) == (M, N)
+    assert_close_to_oracle(out, ref, "config1")
+
+
+LLAMA_SHAPES = [(4096, 6144), (4096, 4096), (4096, 28672), (14336, 4096)]  # (K, N)
+
+
+@pytest.mark.parametrize("K,N", LLAMA_SHAPES)
+def test_config2_decode_sweep(kernels, oracle, dev, K, N):
+    """GPTQ sym int4 g128 at the four Llama-3-8B layer shapes, M in {1,2,4,8,16},
+    activations with 0.1% x50 outlier channels. Every M is checked in full against the oracle."""
+    g = 128
+    x = synth.activations(16, K, seed=200 + K + N, outliers=True)
+    w, s, _ = synth.int4_weight(N, K, g, seed=201 + K + N, asym=False)
+    ref = _oracle_dense(oracle, x, w, s, None, g)  # per-row quant: rows of M=16 == rows of any prefix
+    tiles = kernels.repack_w4(w.to(dev))
+    sd = s.to(dev)
+    xd = x.to(dev)
+    for M in (1, 2, 4, 8, 16):
+        out = kernels.w4a8_linear(xd[:M].contiguous(), tiles, sd, None, g)
+        _sync()
+        assert_close_to_oracle(out, ref[:M], f"K={K} N={N} M={M}")
+
+
+def test_decode_accepts_op_layout_and_explicit_zeros(kernels, oracle, dev):
+    """Op-layout weights are repacked on the call; GPTQ's materialised zeros (all 8) give the same
+    numbers as the symmetric (None) form."""
+    M, K, N, g = 3, 1024, 256, 128
+    x = synth.activations(M, K, seed=5)
+    w, s, _ = synth.int4_weight(N, K, g, seed=6, asym=False)
+    z8 = synth.pack_rows(torch.full((K // g, N), 8, dtype=torch.int32))
+    ref = _oracle_dense(oracle, x, w, s, None, g)
+    a = kernels.w4a8_linear(x.to(dev), w.to(dev), s.to(dev), None, g)
+    b = kernels.w4a8_linear(x.to(dev), w.to(dev), s.to(dev), z8.to(dev), g)
+    _sync()
+    assert_close_to_oracle(a, ref, "sym None")
+    assert_close_to_oracle(b, ref, "sym zeros=8")
+
+
+@pytest.mark.parametrize("g,asym", [(32, True), (64, False), (256, True)])
+def test_decode_group_sizes(kernels, oracle, dev, g, asym):
+    M, K, N = 5, 1536, 128
+    x = synth.activations(M, K, seed=g)
+    w, s, z = synth.int4_weight(N, K, g, seed=g + 1, asym=asym)
+    ref = _oracle_dense(oracle, x, w, s, z, g)
+    out = kernels.w4a8_linear(x.to(dev), w.to(dev), s.to(dev), None if z is None else z.to(dev), g)
+    _sync()
+    assert_close_to_oracle(out, ref, f"g={g}")
+
+
+def test_decode_fp16_activations(kernels, oracle, dev):
+    M, K, N, g = 4, 2048, 256, 128
+    x = synth.activations(M, K, seed=77, dtype=torch.float16)
+    w, s, z = synth.int4_weight(N, K, g, seed=78, asym=True)
+    ref = _oracle_dense(oracle, x, w, s, z, g)
+    out = kernels.w4a8_linear(x.to(dev), w.to(dev), s.to(dev), z.to(dev), g)
+    _sync()
+    assert out.dtype == torch.float16
+    assert_close_to_oracle(out, ref, "fp16")
+
+
+# ------------------------------------------------------------------------------- prefill GEMM
+@pytest.mark.parametrize("K,N", LLAMA_SHAPES)
+def test_config3_prefill(kernels, oracle, dev, K, N):
+    """the same shapes at M in {512, 2048, 8192} on the MFMA arm. A row subset
+    of each run is checked against the oracle; every row must equal the row computed alone
+    (bit-exact row-split / M-invariance)."""
+    g = 128
+    w, s, _ = synth.int4_weight(N, K, g, seed=300 + K + N, asym=False)
+    tiles = kernels.repack_w4(w.to(dev))
+    sd = s.to(dev)
+    for M in (512, 2048, 8192):
+        x = synth.activations(M, K, seed=301 + M, outliers=True)
+        xd = x.to(dev)
+        out = kernels.w4a8_linear(xd, tiles, sd, None, g)
+        rows = torch.tensor(sorted({0, 1, 17, M // 3, M // 2 + 5, M - 2, M - 1}))
+        part = kernels.w4a8_linear(xd[rows].contiguous(), tiles, sd, None, g, kernel="wmma_tiled_tuned")
+        _sync()
+        assert torch.equal(out[rows.to(dev)], part), f"row-split invariance broken at M={M}"
+        ref = _oracle_dense(oracle, x[rows], w, s, None, g)
+        assert_close_to_oracle(part, ref, f"prefill K={K} N={N} M={M}")
+
+
+def test_prefill_asym_ragged(kernels, oracle, dev):
+    """Zero points, M not a multiple of the tile, K not a multiple of 128, N not a multiple of 128."""
+    M, K, N, g = 77, 1184, 208, 32
+    x = synth.activations(M, K, seed=9)
+    w, s, z = synth.int4_weight(N, K, g, seed=10, asym=True)
+    ref = _oracle_dense(oracle, x, w, s, z, g)
+    out = kernels.w4a8_linear(x.to(dev), w.to(dev), s.to(dev), z.to(dev), g)
+    _sync()
+    assert_close_to_oracle(out, ref, "prefill ragged")
+
+
+def test_decode_and_prefill_arms_agree(kernels, oracle, dev):
+    M, K, N, g = 16, 4096, 1024, 128
+    x = synth.activations(M, K, seed=41)
+    w, s, _ = synth.int4_weight(N, K, g, seed=42, asym=False)
+    tiles = kernels.repack_w4(w.to(dev))
+    a = kernels.w4a8_linear(x.to(dev), tiles, s.to(dev), None, g, kernel="decode_gemv")
+    b = kernels.w4a8_linear(x.to(dev), tiles, s.to(dev), None, g, kernel="wmma_tiled_tuned")
+    _sync()
+    ref = _oracle_dense(oracle, x, w, s, None, g)
+    assert_close_to_oracle(a, ref, "decode arm")
+    assert_close_to_oracle(b, ref, "prefill arm")
+
+
+# ------------------------------------------------------------------------------- MXFP4
+@pytest.mark.parametrize("K,N", [(8192, 28672), (28672, 8192)])
+def test_config5_mxfp4(kernels, oracle, dev, K, N):
+    """e2m1 codes, E8M0 block-32 scales (exponents in [-8, 0]), M in {1, 16, 4096}."""
+    w, s8 = synth.mxfp4_weight(N, K, seed=500 + K)
+    tiles = kernels.repack_w4(w.to(dev), weight_is_e2m1=True)
+    sd = s8.to(dev)
+    x = synth.activations(16, K, seed=501 + K)
+    ref = _oracle_dense(oracle, x, w, s8, None, 32, e2m1=True)
+    for M in (1, 16):
+        out = kernels.w4a8_linear(x[:M].contiguous().to(dev), tiles, sd, None, 32, weight_is_e2m1=True)
+        _sync()
+        assert_close_to_oracle(out, ref[:M], f"mxfp4 K={K} N={N} M={M}")
+    M = 4096
+    xb = synth.activations(M, K, seed=502 + K)
+    xd = xb.to(dev)
+    out = kernels.w4a8_linear(xd, tiles, sd, None, 32, weight_is_e2m1=True)
+    rows = torch.tensor([0, 5, 1000, 2047, 4095])
+    part = kernels.w4a8_linear(xd[rows].contiguous(), tiles, sd, None, 32, kernel="wmma_tiled_tuned",
+                               weight_is_e2m1=True)
+    _sync()
+    assert torch.equal(out[rows.to(dev)], part)
+    assert_close_to_oracle(part, _oracle_dense(oracle, xb[rows], w, s8, None, 32, e2m1=True), "mxfp4 M=4096")
+
+
+def test_e2m1_with_fp16_group_scales(kernels, oracle, dev):
+    """The fp16-folded MXFP4 scale form (python/minisgl/quant/mxfp4.py:71-97) on both arms."""
+    K, N = 1024, 256
+    w, s8 = synth.mxfp4_weight(N, K, seed=61)
+    s16 = torch.pow(2.0, s8.float() - 127).to(torch.float16)
+    for M in (3, 40):
+        x = synth.activations(M, K, seed=62 + M)
+        ref = _oracle_dense(oracle, x, w, s8, None, 32, e2m1=True)
+        out = kernels.w4a8_linear(x.to(dev), w.to(dev), s16.to(dev), None, 32, weight_is_e2m1=True)
+        _sync()
+        assert_close_to_oracle(out, ref, f"e2m1 fp16-scale M={M}")
+
+
+# ------------------------------------------------------------------------------- fused silu
+SILU_SHAPES = [(1, 256, 512, 128), (2, 512, 1024, 128), (4, 768, 2048, 128), (1, 512, 1536, 128), (1, 384, 1024, 32)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("fmt", ["sym", "asym", "e2m1"])
+def test_fused_silu_bit_exact(kernels, dev, dtype, fmt):
+    """tools/w4a8_gemm_silu_parity.py: fused == unfused decode GEMV + round-silu-round-mul replica,
+    bit for bit."""
+    for (M, inter, K, g) in SILU_SHAPES:
+        N = 2 * inter
+        x = (synth.activations(M, K, seed=M + inter + K, dtype=torch.float32) * 0.3).to(dtype).to(dev)
+        if fmt == "e2m1":
+            if g != 32:
+                continue
+            w, s = synth.mxfp4_weight(N, K, seed=inter)
+            z = None
+        else:
+            w, s, z = synth.int4_weight(N, K, g, seed=inter, asym=fmt == "asym", scale_floor=0.001)
+        w, s = w.to(dev), s.to(dev)
+        z = None if z is None else z.to(dev)
+        e2 = fmt == "e2m1"
+        out1 = kernels.w4a8_linear(x, w, s, z, g, kernel="decode_gemv", weight_is_e2m1=e2)
+        gh, uh = out1[:, :inter], out1[:, inter:]
+        ref = (gh.float() / (1.0 + torch.exp(-gh.float()))).to(dtype) * uh
+        fused = kernels.w4a8_linear_silu(x, w, s, z, g, weight_is_e2m1=e2)
+        _sync()
+        assert torch.equal(fused, ref), f"{fmt} {dtype} M={M} inter={inter} K={K} g={g}: max " \
+                                        f"{(fused.float() - ref.float()).abs().max().item():.3e}"
+
+
+# ------------------------------------------------------------------------------- producer pair
+@pytest.mark.parametrize("M", [1, 17, 129])
+def test_producer_pair_bit_identical(kernels, dev, M):
+    K, N, g = 2048, 512, 128
+    x = synth.activations(M, K, seed=M).to(dev)
+    w, s, _ = synth.int4_weight(N, K, g, seed=M + 1, asym=False)
+    tiles, sd = kernels.repack_w4(w.to(dev)), s.to(dev)
+    q, sc = kernels.act_quant(x)
+    base = kernels.w4a8_linear(x, tiles, sd, None, g)
+    pre = kernels.w4a8_linear(x, tiles, sd, None, g, x_fp8=q, act_scales=sc)
+    pre8 = kernels.w4a8_linear(x, tiles, sd, None, g, x_fp8=q.view(torch.float8_e4m3fn), act_scales=sc)
+    _sync()
+    assert torch.equal(base, pre) and torch.equal(base, pre8)
+
+
+def test_dispatch_ledger_records_arms(kernels, dev):
+    eng = pkg("_hip_engage")
+    K, N, g = 1024, 128, 128
+    w, s, _ = synth.int4_weight(N, K, g, seed=1, asym=False)
+    tiles, sd = kernels.repack_w4(w.to(dev)), s.to(dev)
+    before = eng.counts()
+    kernels.w4a8_linear(synth.activations(2, K, seed=1).to(dev), tiles, sd, None, g)
+    kernels.w4a8_linear(synth.activations(40, K, seed=1).to(dev), tiles, sd, None, g)
+    _sync()
+    d = eng.counts_delta(before)
+    assert d.get("w4a8_mi355x.gemm(decode_gemv)") == 1 and d.get("w4a8_mi355x.gemm(wmma_tiled_tuned)") == 1
