@@ -1,0 +1,258 @@
+"""W4A8 decode-GEMV sweep benchmark on one MI355X.
+
+One step = the W4A8 quantized linear (per-token fp8 act-quant + int4 x fp8 GEMM, bf16 out) at the
+four Llama-3-8B layer shapes (qkv 4096x6144, o_proj 4096x4096, gate_up 4096x28672, down 14336x4096)
+for every M in {1, 2, 4, 8, 16}: 20 calls, captured once into a HIP graph and replayed. Weights are
+GPTQ-symmetric int4 group 128 with fp16 scales |N(0, 0.02)|, activations bf16 N(0,1) with 0.1% of
+channels x50; 5 copies of the weight set are cycled (each M uses its own copy, 555 MB of weights
+per step) so no step re-reads weights out of the 256 MB Infinity Cache.
+
+value = algorithmic bytes of the step (codes N*K/2 + fp16 scales + bf16 x in + bf16 out) x steps /
+wall time, with everything resident in HBM. The roofline object is the decode GEMV kernel alone at
+the largest shape (gate_up, M=1, one launch per call): algorithmic bytes per launch / mean launch
+time from HIP events on the launch stream, against 8 TB/s. cpu_baseline is the reference's
+dequantize-then-matmul CPU path (oracle/baseline.py) on a bounded sample, rank 0 only.
+
+Modes for profiling runs (same committed file): --profile-kernel runs only the roofline loop,
+--copy-calib runs a plain device copy of known size (for scaling rocprofv3 byte counters).
+"""
+from __future__ import annotations
+
+import argparse
+import importlib
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+for p in (str(REPO), str(REPO / "tests")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+SHAPES = [(4096, 6144), (4096, 4096), (4096, 28672), (14336, 4096)]  # (K, N)
+MS = [1, 2, 4, 8, 16]
+GROUP = 128
+HBM_PEAK_GBS = 8000.0
+FP8_PEAK_TFLOPS = 5000.0
+METRIC = "W4A8 GEMM HBM GB/s (M<=16) and TFLOPS (M>=2048), % roofline, 1 MI355X"
+
+
+def algo_bytes(M: int, K: int, N: int) -> int:
+    return N * K // 2 + (K // GROUP) * N * 2 + M * K * 2 + M * N * 2
+
+
+def make_weights(kernels, K: int, N: int, gen, dev):
+    import torch
+
+    codes = torch.randint(0, 16, (N, K), generator=gen, device=dev, dtype=torch.int32)
+    sh = torch.arange(0, 32, 4, dtype=torch.int32, device=dev)
+    w = (codes.view(N, K // 8, 8) << sh).sum(-1, dtype=torch.int32)
+    del codes
+    s = (torch.randn(K // GROUP, N, generator=gen, device=dev).abs() * 0.02).to(torch.float16)
+    tiles = kernels.repack_w4(w)
+    del w
+    return tiles, s
+
+
+def make_x(M: int, K: int, seed: int, dev):
+    import synth
+
+    return synth.activations(M, K, seed=seed, outliers=True).to(dev)
+
+
+def cpu_baseline_leg() -> dict:
+    from oracle import baseline
+
+    r = baseline.run(SHAPES, MS, GROUP, seed=1)
+    gbs = r["bytes"] / r["seconds"] / 1e9
+    return {"value": round(gbs, 4), "unit": "GB/s", "cores": r["cores"], "kind": "port",
+            "sample": f"one full sweep step (4 Llama-3-8B shapes x M in {{1,2,4,8,16}}), {r['bytes'] / 1e6:.0f} MB "
+                      f"algorithmic; per call: per-token e4m3 round trip + int4 dequant to f32 (total "
+                      f"{r['dequant_s']:.2f} s) + f32 matmul ({r['matmul_s']:.2f} s); torch CPU, {r['cores']} threads"}
+
+
+def roofline_leg(kernels, dev, reps: int = 60) -> dict:
+    """Mean launch time of the decode GEMV at gate_up (K=4096, N=28672), M=1, pre-quantized input,
+    cycling 10 weight copies (590 MB) so every launch streams from HBM."""
+    import torch
+
+    K, N = 4096, 28672
+    gen = torch.Generator(device=dev).manual_seed(7)
+    copies = [make_weights(kernels, K, N, gen, dev) for _ in range(10)]
+    x = make_x(1, K, 70, dev)
+    q, s = kernels.act_quant(x)
+    for i in range(10):  # warm
+        t, sc = copies[i % 10]
+        kernels.w4a8_linear(x, t, sc, None, GROUP, x_fp8=q, act_scales=s)
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+    torch.cuda._sleep(200_000_000)  # keep the GPU busy while the launches queue up
+    for i in range(reps):
+        t, sc = copies[i % 10]
+        starts[i].record()
+        kernels.w4a8_linear(x, t, sc, None, GROUP, x_fp8=q, act_scales=s)
+        ends[i].record()
+    torch.cuda.synchronize()
+    durs = sorted(a.elapsed_time(b) * 1e3 for a, b in zip(starts, ends))  # us
+    mean_us = sum(durs) / len(durs)
+    nbytes = algo_bytes(1, K, N) - 1 * K * 2 + 1 * K  # this launch reads fp8 x (1 B/elt), not bf16
+    achieved = nbytes / (mean_us * 1e-6) / 1e9
+    traffic = None
+    tf = REPO / "profiles" / "gemv_gate_up_m1_traffic.json"
+    if tf.exists():
+        traffic = json.loads(tf.read_text()).get("traffic_bytes_per_launch")
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "kernel": "gemv_kernel<1,0> (decode GEMV, int4) K=4096 N=28672 M=1",
+            "algorithmic_bytes_per_launch": nbytes, "mean_launch_us": round(mean_us, 3),
+            "median_launch_us": round(durs[len(durs) // 2], 3)}
+
+
+def prefill_leg(kernels, dev) -> dict:
+    """TFLOPS of the MFMA GEMM at config-3 shapes (M=2048 and M=8192), one warm + timed calls."""
+    import torch
+
+    out = {}
+    gen = torch.Generator(device=dev).manual_seed(9)
+    for K, N in SHAPES:
+        tiles, sc = make_weights(kernels, K, N, gen, dev)
+        for M in (2048, 8192):
+            x = make_x(M, K, 90 + M, dev)
+            q, s = kernels.act_quant(x)
+            kernels.w4a8_linear(x, tiles, sc, None, GROUP, x_fp8=q, act_scales=s)
+            torch.cuda.synchronize()
+            reps = 5
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(reps):
+                kernels.w4a8_linear(x, tiles, sc, None, GROUP, x_fp8=q, act_scales=s)
+            b.record()
+            torch.cuda.synchronize()
+            us = a.elapsed_time(b) * 1e3 / reps
+            tflops = 2.0 * M * N * K / (us * 1e-6) / 1e12
+            out[f"{K}x{N}_M{M}"] = {"us": round(us, 1), "tflops": round(tflops, 1),
+                                    "frac_fp8_peak": round(tflops / FP8_PEAK_TFLOPS, 4)}
+        del tiles, sc
+    return out
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--profile-kernel", action="store_true")
+    ap.add_argument("--copy-calib", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build measures one MI355X; --gpus {args.gpus} (WORLD_SIZE={world}) is not run. "
+              f"Multi-GPU sharding of the path is described in DESIGN.md.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py: no HIP device", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda:0")
+    kernels = importlib.import_module("minisglang-rdna4_amd.quant.kernels")
+
+    if args.copy_calib:
+        n = 256 << 20
+        a = torch.empty(n, dtype=torch.uint8, device=dev)
+        b = torch.empty(n, dtype=torch.uint8, device=dev)
+        for _ in range(5):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calib_bytes_read": n, "copy_calib_bytes_written": n}))
+        return 0
+    if args.profile_kernel:
+        r = roofline_leg(kernels, dev)
+        print(json.dumps(r))
+        return 0
+
+    # ---- sweep setup: 5 weight copies (one per M), activations per (M, shape)
+    gen = torch.Generator(device=dev).manual_seed(1234)
+    weights = [[make_weights(kernels, K, N, gen, dev) for (K, N) in SHAPES] for _ in MS]
+    xs = [[make_x(M, K, 1000 + 10 * i + j, dev) for j, (K, N) in enumerate(SHAPES)] for i, M in enumerate(MS)]
+    step_bytes = sum(algo_bytes(M, K, N) for M in MS for (K, N) in SHAPES)
+    weight_bytes = sum(t.numel() + s.numel() * 2 for row in weights for (t, s) in row)
+
+    def step():
+        outs = []
+        for i, M in enumerate(MS):
+            for j, (K, N) in enumerate(SHAPES):
+                t, s = weights[i][j]
+                outs.append(kernels.w4a8_linear(xs[i][j], t, s, None, GROUP))
+        return outs
+
+    # eager warm-up, then capture one step
+    step()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        graph_outs = step()
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    del graph_outs
+    ms_per_step = elapsed * 1e3 / args.steps
+    value = step_bytes * args.steps / elapsed / 1e9
+
+    # per-shape GEMV-only view (events around graph replays of one call each would add a graph per
+    # shape; the roofline leg covers the dominant shape)
+    roof = roofline_leg(kernels, dev)
+    prefill = None if args.no_prefill else prefill_leg(kernels, dev)
+    cpu = None if args.no_cpu_baseline else cpu_baseline_leg()
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8-e4m3 x int4, f32 accumulate",
+        "data": "synthetic (seeded): GPTQ-sym int4 g128 codes U{0..15}, fp16 scales |N(0,0.02)|, bf16 N(0,1) "
+                "activations with 0.1% channels x50",
+        "config": {
+            "workload": "configs[1]: decode W4A8 GEMM sweep at Llama-3-8B layer shapes, M in {1,2,4,8,16}; one step = "
+                        "20 calls (act-quant + GEMM each), HIP-graph replayed",
+            "shapes_KxN": [f"{K}x{N}" for K, N in SHAPES],
+            "M": MS,
+            "group_size": GROUP,
+            "algorithmic_bytes_per_step": step_bytes,
+            "weight_bytes_cycled": weight_bytes,
+            "frac_of_hbm_peak_whole_step": round(value / HBM_PEAK_GBS, 4),
+        },
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "prefill_config3": prefill,
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,56 @@
+"""CPU baseline for bench.py -- TEST INFRASTRUCTURE ONLY (the cpu_baseline leg).
+
+Restates the reference's CPU dequantize-then-matmul path for W4A8 (tools/moe_parity.py:23-43,
+tools/qwen3_5_moe_awq_convert_test.py:40-69, python/minisgl/quant/mxfp4.py:262-275): quantize x per
+token to e4m3 and back to f32, dequantize W = scale * (q - zero) to an f32 (N, K) matrix, then an
+f32 matmul. torch on the CPU, all host cores.
+"""
+from __future__ import annotations
+
+import os
+import time
+
+import torch
+
+
+def _e4m3_roundtrip(x: torch.Tensor) -> torch.Tensor:
+    xf = x.float()
+    amax = xf.abs().amax(dim=1, keepdim=True)
+    s = (amax / 448.0).clamp_min(1e-8)
+    q = (xf * (1.0 / s)).to(torch.float8_e4m3fn)
+    return q.float() * s
+
+
+def _dequant_int4(w_packed: torch.Tensor, scales: torch.Tensor, group: int) -> torch.Tensor:
+    N, K8 = w_packed.shape
+    sh = torch.arange(0, 32, 4, dtype=torch.int32)
+    q = ((w_packed.unsqueeze(-1) >> sh) & 15).reshape(N, K8 * 8).float()
+    return (q - 8.0) * scales.float().t().repeat_interleave(group, dim=1)
+
+
+def run(shapes, Ms, group: int, seed: int = 0) -> dict:
+    """Times the reference CPU path for every (K, N) shape at every M (one call = act round trip +
+    dequant + matmul, as each reference CPU call dequantizes); returns bytes, seconds, cores."""
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    g = torch.Generator().manual_seed(seed)
+    t_deq = t_mm = 0.0
+    nbytes = 0
+    for K, N in shapes:
+        codes = torch.randint(0, 16, (N, K), generator=g, dtype=torch.int32)
+        w = ((codes.reshape(N, K // 8, 8) << torch.arange(0, 32, 4, dtype=torch.int32)).sum(-1)).to(torch.int32)
+        s = (torch.randn(K // group, N, generator=g).abs() * 0.02).to(torch.float16)
+        del codes
+        for M in Ms:
+            x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+            t0 = time.perf_counter()
+            xd = _e4m3_roundtrip(x)
+            wd = _dequant_int4(w, s, group)
+            t1 = time.perf_counter()
+            y = (xd @ wd.t()).to(torch.bfloat16)
+            t2 = time.perf_counter()
+            t_deq += t1 - t0
+            t_mm += t2 - t1
+            nbytes += N * K // 2 + (K // group) * N * 2 + M * K * 2 + M * N * 2
+            del y, wd
+    return {"bytes": nbytes, "seconds": t_deq + t_mm, "dequant_s": t_deq, "matmul_s": t_mm, "cores": cores}
