@@ -74,18 +74,18 @@ def cpu_baseline_leg() -> dict:
 
 
 def roofline_leg(kernels, dev, reps: int = 60) -> dict:
-    """Mean launch time of the decode GEMV at gate_up (K=4096, N=28672), M=1, pre-quantized input,
-    cycling 10 weight copies (590 MB) so every launch streams from HBM."""
+    """Mean launch time of the decode GEMV at gate_up (K=4096, N=28672), M=1, bf16 input quantized
+    in the kernel's prologue (the product's decode path: one launch per call), cycling 10 weight
+    copies (590 MB) so every launch streams from HBM."""
     import torch
 
     K, N = 4096, 28672
     gen = torch.Generator(device=dev).manual_seed(7)
     copies = [make_weights(kernels, K, N, gen, dev) for _ in range(10)]
     x = make_x(1, K, 70, dev)
-    q, s = kernels.act_quant(x)
     for i in range(10):  # warm
         t, sc = copies[i % 10]
-        kernels.w4a8_linear(x, t, sc, None, GROUP, x_fp8=q, act_scales=s)
+        kernels.w4a8_linear(x, t, sc, None, GROUP)
     torch.cuda.synchronize()
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
@@ -93,12 +93,12 @@ def roofline_leg(kernels, dev, reps: int = 60) -> dict:
     for i in range(reps):
         t, sc = copies[i % 10]
         starts[i].record()
-        kernels.w4a8_linear(x, t, sc, None, GROUP, x_fp8=q, act_scales=s)
+        kernels.w4a8_linear(x, t, sc, None, GROUP)
         ends[i].record()
     torch.cuda.synchronize()
     durs = sorted(a.elapsed_time(b) * 1e3 for a, b in zip(starts, ends))  # us
     mean_us = sum(durs) / len(durs)
-    nbytes = algo_bytes(1, K, N) - 1 * K * 2 + 1 * K  # this launch reads fp8 x (1 B/elt), not bf16
+    nbytes = algo_bytes(1, K, N)
     achieved = nbytes / (mean_us * 1e-6) / 1e9
     traffic = None
     tf = REPO / "profiles" / "gemv_gate_up_m1_traffic.json"
@@ -106,7 +106,7 @@ def roofline_leg(kernels, dev, reps: int = 60) -> dict:
         traffic = json.loads(tf.read_text()).get("traffic_bytes_per_launch")
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-            "kernel": "gemv_kernel<1,0> (decode GEMV, int4) K=4096 N=28672 M=1",
+            "kernel": "gemv_kernel<1,CH,kModeI4,kAQuant,SYM> (decode GEMV, int4 sym, fused act quant) K=4096 N=28672 M=1",
             "algorithmic_bytes_per_launch": nbytes, "mean_launch_us": round(mean_us, 3),
             "median_launch_us": round(durs[len(durs) // 2], 3)}
 

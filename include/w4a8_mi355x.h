@@ -72,6 +72,22 @@ int w4a8_gemm(const uint8_t* x_fp8, int64_t ldx, const float* act_scales, int64_
               void* out, int out_dtype, int64_t ldo, int silu, void* workspace, int64_t workspace_bytes, int kernel,
               void* stream);
 
+/* Workspace bytes w4a8_linear may need for M rows of K inputs (the fp8 codes and scales of x when
+ * they are not produced inside the GEMM kernel); -1 on bad sizes. */
+int64_t w4a8_linear_workspace_bytes(int64_t M, int64_t K);
+
+/* Dense W4A8 linear on bf16/fp16 activations x (M, ldx): per-token fp8 quant of x, then the GEMM of
+ * w4a8_gemm, with the same outputs bit for bit as w4a8_act_quant followed by w4a8_gemm. This is
+ * fp8_wmma.mmq_fp8_gemm / mmq_fp8_gemm_silu called without a producer pair, which quantize in-op
+ * (python/minisgl/quant/kernels.py:1686-1753, in-op quant :1703-1712). For decode-sized calls
+ * whose rows fit the kernel's LDS (rows x K up to about 16K elements) the quant runs in the GEMV
+ * kernel's prologue and the call is a single launch; otherwise one act-quant launch writes the
+ * workspace (w4a8_linear_workspace_bytes, 16-byte aligned) first. */
+int w4a8_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const void* w_tile, int64_t N,
+                const void* scales, int scale_fmt, const int32_t* zeros, int wfmt, int64_t group_size, void* out,
+                int out_dtype, int64_t ldo, int silu, void* workspace, int64_t workspace_bytes, int kernel,
+                void* stream);
+
 /* Softmax + top-k (ties keep the lower expert index) + optional renormalisation. Replaces the
  * route half of moe_hip.moe_route_align (python/minisgl/quant/kernels.py:423-447; tie rule
  * python/minisgl/layers/moe.py:1218-1227). E <= 512. */

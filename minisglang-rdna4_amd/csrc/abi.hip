@@ -12,7 +12,8 @@ namespace w4a8 {
 int launch_act_quant(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx, uint8_t* q,
                      int64_t ldq, float* scales, const int32_t* row_count, hipStream_t stream);
 int launch_repack(const int32_t* w, int64_t N, int64_t K, int wfmt, void* out, hipStream_t stream);
-int launch_gemv(GemmArgs p, int64_t row_blocks, hipStream_t stream);
+int launch_gemv(GemmArgs p, int64_t row_blocks, bool quant_src, hipStream_t stream);
+bool gemv_can_fuse_quant(const GemmArgs& p, int64_t row_blocks);
 size_t gemv_workspace_bytes(int64_t M, int64_t N, int64_t K, int grouped, int64_t row_blocks);
 int launch_prefill(const GemmArgs& p, int64_t rows_to_cover, int bm_rows, hipStream_t stream);
 int launch_moe_route(const void* logits, int dtype, int64_t T, int E, int top_k, int renorm, float* tw,
@@ -61,8 +62,8 @@ static int check_weights(const char* who, int64_t N, int64_t K, int scale_fmt, c
   if (wfmt != kInt4 && wfmt != kE2M1) return fail(kErrInvalid, "%s: unknown weight format %d", who, wfmt);
   if (scale_fmt != kScaleF16 && scale_fmt != kScaleE8M0)
     return fail(kErrInvalid, "%s: unknown scale format %d", who, scale_fmt);
-  if (!(group == 32 || group == 64 || (group >= 128 && group % 128 == 0)))
-    return fail(kErrUnsupported, "%s: group_size=%lld unsupported (32, 64 or a multiple of 128)", who, (long long)group);
+  if (!(group == 32 || group == 64 || (group >= 128 && (group & (group - 1)) == 0)))
+    return fail(kErrUnsupported, "%s: group_size=%lld unsupported (32, 64 or a power of two >= 128)", who, (long long)group);
   if (K % group) return fail(kErrInvalid, "%s: K=%lld is not a multiple of group_size=%lld", who, (long long)K, (long long)group);
   if (wfmt == kE2M1 && zeros) return fail(kErrInvalid, "%s: e2m1 weights are symmetric; w_zeros must be empty", who);
   if (scale_fmt == kScaleE8M0 && wfmt != kE2M1)
@@ -108,43 +109,95 @@ int64_t w4a8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int kernel) {
   return (int64_t)gemv_workspace_bytes(M, N, K, 0, (M + 15) / 16);
 }
 
-int w4a8_gemm(const uint8_t* x_fp8, int64_t ldx, const float* act_scales, int64_t M, const void* w_tile, int64_t N,
-              int64_t K, const void* scales, int scale_fmt, const int32_t* zeros, int wfmt, int64_t group_size,
-              void* out, int out_dtype, int64_t ldo, int silu, void* workspace, int64_t workspace_bytes, int kernel,
-              void* stream) {
-  int rc = check_weights("w4a8_gemm", N, K, scale_fmt, zeros, wfmt, group_size);
-  if (rc) return rc;
-  if (M < 0) return fail(kErrInvalid, "w4a8_gemm: M=%lld", (long long)M);
-  if (M == 0) return kOk;
-  if (ldx < K || ldx % 16 || !aligned16(x_fp8))
-    return fail(kErrInvalid, "w4a8_gemm: x_fp8 rows must be 16-byte aligned with stride >= K (ldx=%lld)", (long long)ldx);
-  if (out_dtype != kBF16 && out_dtype != kF16 && out_dtype != kF32)
-    return fail(kErrInvalid, "w4a8_gemm: unknown output dtype %d", out_dtype);
-  if (silu && (N % 32)) return fail(kErrInvalid, "w4a8_gemm: fused silu needs N=2*inter with inter %% 16 == 0 (N=%lld)", (long long)N);
-  if (silu && out_dtype == kF32) return fail(kErrInvalid, "w4a8_gemm: fused silu rounds through bf16/fp16; f32 output unsupported");
-  const int64_t nout = silu ? N / 2 : N;
-  if (ldo < nout) return fail(kErrInvalid, "w4a8_gemm: ldo=%lld < output width %lld", (long long)ldo, (long long)nout);
-  if (!aligned16(w_tile)) return fail(kErrInvalid, "w4a8_gemm: weight tiles must be 16-byte aligned");
-  if (kernel < 0 || kernel > 2) return fail(kErrInvalid, "w4a8_gemm: kernel must be 0 (auto), 1 (decode) or 2 (prefill)");
-  const bool decode = kernel == 1 || (kernel == 0 && M <= kGemvMaxRows);
+}  // extern "C"
 
-  GemmArgs p = {};
-  p.xq = x_fp8; p.ldx = ldx; p.act_scales = act_scales; p.M = M;
+// Checks shared by w4a8_gemm and w4a8_linear; fills the dense GEMM arguments (A fields left empty).
+static int dense_args(const char* who, int64_t M, const void* w_tile, int64_t N, int64_t K, const void* scales,
+                      int scale_fmt, const int32_t* zeros, int wfmt, int64_t group_size, void* out, int out_dtype,
+                      int64_t ldo, int silu, int kernel, GemmArgs& p) {
+  int rc = check_weights(who, N, K, scale_fmt, zeros, wfmt, group_size);
+  if (rc) return rc;
+  if (M < 0) return fail(kErrInvalid, "%s: M=%lld", who, (long long)M);
+  if (out_dtype != kBF16 && out_dtype != kF16 && out_dtype != kF32)
+    return fail(kErrInvalid, "%s: unknown output dtype %d", who, out_dtype);
+  if (silu && (N % 32)) return fail(kErrInvalid, "%s: fused silu needs N=2*inter with inter %% 16 == 0 (N=%lld)", who, (long long)N);
+  if (silu && out_dtype == kF32) return fail(kErrInvalid, "%s: fused silu rounds through bf16/fp16; f32 output unsupported", who);
+  const int64_t nout = silu ? N / 2 : N;
+  if (ldo < nout) return fail(kErrInvalid, "%s: ldo=%lld < output width %lld", who, (long long)ldo, (long long)nout);
+  if (!aligned16(w_tile)) return fail(kErrInvalid, "%s: weight tiles must be 16-byte aligned", who);
+  if (kernel < 0 || kernel > 2) return fail(kErrInvalid, "%s: kernel must be 0 (auto), 1 (decode) or 2 (prefill)", who);
+  p = GemmArgs{};
+  p.M = M;
   p.N = N; p.K = K; p.KT = (K + 127) / 128;
   p.wt = reinterpret_cast<const uint4*>(w_tile);
   p.scales = scales; p.sfmt = scale_fmt; p.zeros = zeros; p.group = (int)group_size; p.wfmt = wfmt;
   p.out = out; p.out_dtype = out_dtype; p.ldo = ldo; p.silu = silu;
   p.top_k = 1; p.bm = 16;
-  if (decode) {
-    const int64_t rb = (M + 15) / 16;
-    const size_t need = gemv_workspace_bytes(M, N, K, 0, rb);
-    if (need > 0 && (workspace == nullptr || (size_t)workspace_bytes < need))
-      return fail(kErrInvalid, "w4a8_gemm: decode split-K needs a %zu-byte workspace, got %lld", need,
-                  (long long)workspace_bytes);
-    p.partial = reinterpret_cast<float*>(workspace);
-    return hip_status(launch_gemv(p, rb, (hipStream_t)stream), "w4a8_gemm(decode)");
-  }
-  return hip_status(launch_prefill(p, M, 128, (hipStream_t)stream), "w4a8_gemm(prefill)");
+  return kOk;
+}
+
+static int run_dense(const char* who, GemmArgs& p, int kernel, hipStream_t stream) {
+  const bool decode = kernel == 1 || (kernel == 0 && p.M <= kGemvMaxRows);
+  char what[96];
+  snprintf(what, sizeof what, "%s(%s)", who, decode ? "decode" : "prefill");
+  if (decode) return hip_status(launch_gemv(p, (p.M + 15) / 16, false, stream), what);
+  return hip_status(launch_prefill(p, p.M, 128, stream), what);
+}
+
+static int64_t round256(int64_t b) { return (b + 255) / 256 * 256; }
+
+extern "C" {
+
+int w4a8_gemm(const uint8_t* x_fp8, int64_t ldx, const float* act_scales, int64_t M, const void* w_tile, int64_t N,
+              int64_t K, const void* scales, int scale_fmt, const int32_t* zeros, int wfmt, int64_t group_size,
+              void* out, int out_dtype, int64_t ldo, int silu, void* workspace, int64_t workspace_bytes, int kernel,
+              void* stream) {
+  (void)workspace; (void)workspace_bytes;
+  GemmArgs p;
+  int rc = dense_args("w4a8_gemm", M, w_tile, N, K, scales, scale_fmt, zeros, wfmt, group_size, out, out_dtype, ldo,
+                      silu, kernel, p);
+  if (rc) return rc;
+  if (M == 0) return kOk;
+  if (ldx < K || ldx % 16 || !aligned16(x_fp8))
+    return fail(kErrInvalid, "w4a8_gemm: x_fp8 rows must be 16-byte aligned with stride >= K (ldx=%lld)", (long long)ldx);
+  p.xq = x_fp8; p.ldx = ldx; p.act_scales = act_scales;
+  return run_dense("w4a8_gemm", p, kernel, (hipStream_t)stream);
+}
+
+int64_t w4a8_linear_workspace_bytes(int64_t M, int64_t K) {
+  if (M < 0 || K <= 0) return -1;
+  return round256(M * K) + round256(M * 4);
+}
+
+int w4a8_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const void* w_tile, int64_t N,
+                const void* scales, int scale_fmt, const int32_t* zeros, int wfmt, int64_t group_size, void* out,
+                int out_dtype, int64_t ldo, int silu, void* workspace, int64_t workspace_bytes, int kernel,
+                void* stream) {
+  GemmArgs p;
+  int rc = dense_args("w4a8_linear", M, w_tile, N, K, scales, scale_fmt, zeros, wfmt, group_size, out, out_dtype,
+                      ldo, silu, kernel, p);
+  if (rc) return rc;
+  if (M == 0) return kOk;
+  if (x_dtype != kBF16 && x_dtype != kF16) return fail(kErrInvalid, "w4a8_linear: x must be bf16 or fp16 (dtype %d)", x_dtype);
+  if (ldx < K || ldx % 8 || !aligned16(x))
+    return fail(kErrInvalid, "w4a8_linear: x rows must be 16-byte aligned with stride >= K (ldx=%lld)", (long long)ldx);
+  const bool decode = kernel == 1 || (kernel == 0 && M <= kGemvMaxRows);
+  const hipStream_t st = (hipStream_t)stream;
+  p.xsrc = reinterpret_cast<const uint16_t*>(x); p.ldxs = ldx; p.xdtype = x_dtype;
+  if (decode && gemv_can_fuse_quant(p, (M + 15) / 16))
+    return hip_status(launch_gemv(p, (M + 15) / 16, true, st), "w4a8_linear(decode, fused quant)");
+  // quantize into the workspace, then the fp8 GEMM
+  const int64_t need = w4a8_linear_workspace_bytes(M, K);
+  if (workspace == nullptr || workspace_bytes < need || !aligned16(workspace))
+    return fail(kErrInvalid, "w4a8_linear: needs a 16-byte aligned workspace of %lld bytes, got %lld", (long long)need,
+                (long long)workspace_bytes);
+  uint8_t* xq = reinterpret_cast<uint8_t*>(workspace);
+  float* xs = reinterpret_cast<float*>(xq + round256(M * K));
+  rc = launch_act_quant(x, x_dtype, M, K, ldx, xq, K, xs, nullptr, st);
+  if (rc) return hip_status(rc, "w4a8_linear(act quant)");
+  p.xsrc = nullptr;
+  p.xq = xq; p.ldx = K; p.act_scales = xs;
+  return run_dense("w4a8_linear", p, kernel, st);
 }
 
 int w4a8_moe_route(const void* logits, int logits_dtype, int64_t T, int64_t E, int top_k, int renormalize,
@@ -218,7 +271,7 @@ int w4a8_moe_gemm(const uint8_t* a_fp8, int64_t lda, const float* a_scales, int 
       return fail(kErrInvalid, "w4a8_moe_gemm: decode split-K needs a %zu-byte workspace, got %lld", need,
                   (long long)workspace_bytes);
     p.partial = reinterpret_cast<float*>(workspace);
-    return hip_status(launch_gemv(p, rb, (hipStream_t)stream), "w4a8_moe_gemm(decode)");
+    return hip_status(launch_gemv(p, rb, false, (hipStream_t)stream), "w4a8_moe_gemm(decode)");
   }
   const int bm_rows = block_m % 128 == 0 ? 128 : 64;
   return hip_status(launch_prefill(p, nblk * block_m, bm_rows, (hipStream_t)stream), "w4a8_moe_gemm(prefill)");

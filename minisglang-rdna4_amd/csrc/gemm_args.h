@@ -9,6 +9,10 @@ struct GemmArgs {
   const uint8_t* xq;
   int64_t ldx;
   const float* act_scales;
+  // bf16/fp16 activations for the decode GEMV's fused quant prologue (null otherwise)
+  const uint16_t* xsrc;
+  int64_t ldxs;       // elements
+  int xdtype;
   int64_t M;          // dense: rows of x/out. grouped: padded row capacity P
   // weights
   int64_t N;          // output channels of the weight (2*inter for the fused-silu arms)

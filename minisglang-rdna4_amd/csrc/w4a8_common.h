@@ -117,6 +117,77 @@ __device__ __forceinline__ float from_dtype(uint16_t h, int dtype) {
   return dtype == kBF16 ? bf16_to_f32(h) : f16_to_f32(h);
 }
 
+// ---- buffer loads: wave-uniform base and size in a resource descriptor (SGPRs), 32-bit per-lane
+// offset, and a scalar offset that the compiler computes with SALU. Loads past `bytes` return 0.
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+typedef __amdgpu_buffer_rsrc_t BufRsrc;
+
+__device__ __forceinline__ BufRsrc make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 bload128(BufRsrc r, uint32_t voff, uint32_t soff) {
+  const v4u v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+// streaming (non-temporal) variant for data read exactly once, such as weight tiles
+__device__ __forceinline__ uint4 bload128_nt(BufRsrc r, uint32_t voff, uint32_t soff) {
+  const v4u v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 2);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint32_t bload32(BufRsrc r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+}
+__device__ __forceinline__ uint16_t bload16(BufRsrc r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
+}
+__device__ __forceinline__ uint8_t bload8(BufRsrc r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b8(r, voff, soff, 0);
+}
+
+// ---- per-token fp8 activation quant pieces (shared by the act-quant kernel and the decode GEMV's
+// fused prologue, so both produce the same codes bit for bit)
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// 8 bf16/fp16 values (one 16-byte load) -> f32
+__device__ __forceinline__ void unpack8(const uint4& u, int dtype, float* f) {
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = from_dtype((uint16_t)(w[i] & 0xffffu), dtype);
+    f[2 * i + 1] = from_dtype((uint16_t)(w[i] >> 16), dtype);
+  }
+}
+
+__device__ __forceinline__ float amax8(const uint4& u, int dtype) {
+  float f[8];
+  unpack8(u, dtype, f);
+  float m = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(f[i]));
+  return m;
+}
+
+// s = max(amax / 448, 1e-8) (IEEE f32 division)
+__device__ __forceinline__ float act_row_scale(float amax) {
+  float s = amax / 448.0f;
+  if (s < 1e-8f) s = 1e-8f;
+  return s;
+}
+
+// 8 values times inv, to e4m3 with round-to-nearest-even (v_cvt_pk_fp8_f32), packed little-endian
+__device__ __forceinline__ uint2 quant8(const float* f, float inv) {
+  uint32_t lo = 0, hi = 0;
+  lo = __builtin_amdgcn_cvt_pk_fp8_f32(f[0] * inv, f[1] * inv, lo, false);
+  lo = __builtin_amdgcn_cvt_pk_fp8_f32(f[2] * inv, f[3] * inv, lo, true);
+  hi = __builtin_amdgcn_cvt_pk_fp8_f32(f[4] * inv, f[5] * inv, hi, false);
+  hi = __builtin_amdgcn_cvt_pk_fp8_f32(f[6] * inv, f[7] * inv, hi, true);
+  return make_uint2(lo, hi);
+}
+
 // A operand: row pointer (already offset to the tile's K start), valid K extent in bytes from
 // the tile start (multiple of 16). Rows with a null pointer give zeros.
 __device__ __forceinline__ v8i load_a_operand(const uint8_t* row, int kvalid, int lane) {

@@ -249,21 +249,31 @@ def _dense(x, w_packed, scales, w_zeros, group_size, weight_is_e2m1, x_fp8, act_
                              f"{w_zeros.dtype} {tuple(w_zeros.shape)}")
     xq, xs = _check_producer_pair(x, x_fp8, act_scales, what)
     tiles = _as_tiles(w_packed, K, weight_is_e2m1, 2, what)
-    if xq is None:
-        xq, xs = act_quant(x)
     nout = N // 2 if silu else N
     out = torch.empty((M, nout), dtype=x.dtype, device=x.device)
     lib = _abi.load()
-    ws_bytes = int(lib.w4a8_gemm_workspace_bytes(M, N, K, arm))
-    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=x.device) if ws_bytes > 0 else None
-    _abi.check(
-        lib.w4a8_gemm(_abi.ptr(xq), K, _abi.ptr(xs), M, _abi.ptr(tiles), N, K, _abi.ptr(scales.contiguous()), sfmt,
-                      _abi.ptr(w_zeros.contiguous() if w_zeros is not None else None),
-                      _abi.W_E2M1 if weight_is_e2m1 else _abi.W_INT4, group_size, _abi.ptr(out),
-                      _abi.dtype_code(x.dtype), nout, int(silu), _abi.ptr(ws), ws_bytes, arm,
-                      _abi.stream_of(x)),
-        what,
-    )
+    zeros = _abi.ptr(w_zeros.contiguous() if w_zeros is not None else None)
+    wfmt = _abi.W_E2M1 if weight_is_e2m1 else _abi.W_INT4
+    sc = scales.contiguous()
+    if xq is None:
+        # the op quantizes x itself: in the decode kernel's prologue when the rows fit, else with
+        # one act-quant launch into the workspace
+        x = x.contiguous()
+        ws_bytes = int(lib.w4a8_linear_workspace_bytes(M, K))
+        ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=x.device)
+        _abi.check(
+            lib.w4a8_linear(_abi.ptr(x), _abi.dtype_code(x.dtype), M, K, K, _abi.ptr(tiles), N, _abi.ptr(sc),
+                            sfmt, zeros, wfmt, group_size, _abi.ptr(out), _abi.dtype_code(x.dtype), nout, int(silu),
+                            _abi.ptr(ws), ws_bytes, arm, _abi.stream_of(x)),
+            what,
+        )
+    else:
+        _abi.check(
+            lib.w4a8_gemm(_abi.ptr(xq), K, _abi.ptr(xs), M, _abi.ptr(tiles), N, K, _abi.ptr(sc), sfmt, zeros, wfmt,
+                          group_size, _abi.ptr(out), _abi.dtype_code(x.dtype), nout, int(silu), None, 0, arm,
+                          _abi.stream_of(x)),
+            what,
+        )
     return out, tiles is not w_packed
 
 

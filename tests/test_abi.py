@@ -35,6 +35,37 @@ def test_header_declares_the_bound_surface():
     assert _declared() == sorted(abi.SIGNATURES)
 
 
+def _declared_params() -> dict[str, list[str]]:
+    """name -> parameter type list, parsed from the header's prototypes."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    out = {}
+    for m in re.finditer(r"^[A-Za-z_][\w\s\*]*?\b(w4a8_\w+)\s*\(([^)]*)\)\s*;", text, re.M):
+        params = [p.strip() for p in m.group(2).replace("\n", " ").split(",") if p.strip()]
+        if params == ["void"]:
+            params = []
+        out[m.group(1)] = [re.sub(r"\s*\b\w+$", "", p) for p in params]
+    return out
+
+
+def _ctype_of(decl: str):
+    decl = decl.replace("const ", "").strip()
+    if "*" in decl:
+        return ctypes.c_void_p if decl not in ("char*", "char *") else ctypes.c_char_p
+    return {"int": ctypes.c_int, "int64_t": ctypes.c_int64}[decl]
+
+
+def test_bindings_match_header_prototypes():
+    """Each ctypes signature has the header's parameter count and kinds (pointer / int / int64)."""
+    abi = pkg("_abi")
+    protos = _declared_params()
+    assert sorted(protos) == _declared()
+    for name, params in protos.items():
+        _, argtypes = abi.SIGNATURES[name]
+        assert len(argtypes) == len(params), f"{name}: binding has {len(argtypes)} args, header {len(params)}"
+        for i, (a, d) in enumerate(zip(argtypes, params)):
+            assert a == _ctype_of(d), f"{name} arg {i}: binding {a}, header {d!r}"
+
+
 def test_library_exports_every_declared_symbol(lib):
     raw = ctypes.CDLL(str(pkg("_abi").lib_path()))
     for name in _declared():
