@@ -1,0 +1,141 @@
+"""GPU: the method layer end to end -- checkpoint-layout buffers, post_load on the device (W4 tiles
+made once), apply / apply_swiglu / MoE apply -- against the operator API called on the op layout
+(bit-identical, both run the same kernels on the same tiles) and against the CPU oracle.
+"""
+from types import SimpleNamespace
+
+import pytest
+import torch
+
+import synth
+from conftest import pkg
+from test_gpu_dense import assert_close_to_oracle
+
+pytestmark = pytest.mark.gpu
+
+M_ = pkg("quant.method")
+C_ = pkg("quant.config")
+L_ = pkg("layers.moe")
+
+AWQ = C_.QuantConfig(method="awq", bits=4, group_size=128, sym=False)
+GPTQ = C_.QuantConfig(method="gptq", bits=4, group_size=128, sym=True)
+MX = C_.QuantConfig(method="compressed-tensors", bits=4, group_size=32, sym=True, weight_type="float",
+                    ct_format="mxfp4-pack-quantized")
+
+
+def _rand_i32(shape, g):
+    return torch.randint(-2**31, 2**31 - 1, shape, generator=g, dtype=torch.int32)
+
+
+def _awq_layer(N, K, seed, dev):
+    g = synth.gen(seed)
+    m = M_.W4A8LinearMethod(AWQ)
+    lay = SimpleNamespace()
+    m.create_weights(lay, N, K)
+    lay.qweight = _rand_i32(lay.qweight.shape, g)
+    lay.scales = (torch.rand(lay.scales.shape, generator=g) * 0.02 + 1e-3).to(torch.float16)
+    lay.qzeros = _rand_i32(lay.qzeros.shape, g)
+    ckpt = (lay.qweight.clone(), lay.scales.clone(), lay.qzeros.clone())
+    for a in ("qweight", "scales", "qzeros"):
+        setattr(lay, a, getattr(lay, a).to(dev))
+    m.process_weights_after_load(lay)
+    return m, lay, ckpt
+
+
+@pytest.mark.parametrize("M", [1, 4, 16, 40])
+def test_awq_linear_method_matches_operator_and_oracle(kernels, oracle, dev, M):
+    N, K = 512, 1024
+    m, lay, (qw, sc, qz) = _awq_layer(N, K, seed=31, dev=dev)
+    assert lay._w_packed_op.dtype == torch.uint8  # W4 tiles, made once at load
+    w_op, s_op, z_op = kernels.awq_to_op_layout(qw, sc, qz)
+    x = synth.activations(M, K, seed=M).to(dev)
+    bias = torch.randn(N, generator=synth.gen(2)).to(torch.bfloat16).to(dev)
+    out = m.apply(lay, x, None)
+    out_b = m.apply(lay, x, bias)
+    ref_op = kernels.w4a8_linear(x, w_op.to(dev), s_op.to(dev), z_op.to(dev), 128)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref_op) and torch.equal(out_b, ref_op + bias)
+    xq, xs = oracle.act_quant(synth.bits16(x.cpu()), 0)
+    ref = oracle.gemm(xq, xs, w_op.numpy(), s_op.numpy(), z_op.numpy(), 128, False)
+    assert_close_to_oracle(out, ref, f"AWQ method M={M}")
+
+
+def test_awq_apply_swiglu_fires_at_decode_and_is_bit_exact(kernels, dev):
+    N, K = 512, 1024  # merged gate_up, inter 256
+    m, lay, _ = _awq_layer(N, K, seed=41, dev=dev)
+    x = synth.activations(4, K, seed=3).to(dev)
+    fused = m.apply_swiglu(lay, x)
+    y = m.apply(lay, x, None)
+    gh, uh = y[:, : N // 2], y[:, N // 2:]
+    ref = (gh.float() / (1.0 + torch.exp(-gh.float()))).to(x.dtype) * uh
+    torch.cuda.synchronize()
+    assert fused is not None and torch.equal(fused, ref)
+    assert m.apply_swiglu(lay, synth.activations(17, K, seed=4).to(dev)) is None  # prefill: caller unfuses
+
+
+def test_gptq_symmetric_method_drops_zeros_and_matches_oracle(kernels, oracle, dev):
+    N, K = 256, 2048
+    g = synth.gen(51)
+    m = M_.W4A8LinearMethod(GPTQ)
+    lay = SimpleNamespace()
+    m.create_weights(lay, N, K)
+    qw = _rand_i32(lay.qweight.shape, g)
+    sc = (torch.rand(lay.scales.shape, generator=g) * 0.02 + 1e-3).to(torch.float16)
+    lay.qweight, lay.scales = qw.to(dev), sc.to(dev)
+    lay.qzeros = torch.full(lay.qzeros.shape, 0x77777777, dtype=torch.int32, device=dev)
+    m.process_weights_after_load(lay)
+    assert lay._zeros_op is None
+    w_op, s_op, _ = kernels.gptq_to_op_layout(qw, sc, torch.full((K // 128, N // 8), 0x77777777, dtype=torch.int32))
+    x = synth.activations(2, K, seed=5).to(dev)
+    out = m.apply(lay, x, None)
+    torch.cuda.synchronize()
+    xq, xs = oracle.act_quant(synth.bits16(x.cpu()), 0)
+    assert_close_to_oracle(out, oracle.gemm(xq, xs, w_op.numpy(), s_op.numpy(), None, 128, False), "GPTQ sym method")
+
+
+def test_mxfp4_linear_method(kernels, oracle, dev):
+    N, K = 256, 1024
+    g = synth.gen(61)
+    codes = torch.randint(0, 16, (N, K), generator=g, dtype=torch.int32)
+    wpk = (codes[:, 0::2] | (codes[:, 1::2] << 4)).to(torch.uint8)
+    ws = torch.randint(119, 128, (N, K // 32), generator=g, dtype=torch.int32).to(torch.uint8)
+    m = M_.create_linear_method(MX)
+    lay = SimpleNamespace(weight_packed=wpk.to(dev), weight_scale=ws.to(dev))
+    m.process_weights_after_load(lay)
+    x = synth.activations(3, K, seed=6).to(dev)
+    out = m.apply(lay, x, None)
+    torch.cuda.synchronize()
+    xq, xs = oracle.act_quant(synth.bits16(x.cpu()), 0)
+    ref = oracle.gemm(xq, xs, synth.pack_rows(codes).numpy(), ws.t().contiguous().numpy(), None, 32, True)
+    assert_close_to_oracle(out, ref, "MXFP4 method")
+
+
+def test_moe_method_matches_operator(kernels, dev):
+    """GPTQ experts through the MoE method == w4a8_moe on the op layout (same route, same tiles)."""
+    E, H, I, T, k = 8, 256, 128, 5, 2
+    g = synth.gen(71)
+    m = L_.create_moe_quant_method(GPTQ)
+    w13, w2 = m.create_experts(E, 2 * I, H), m.create_experts(E, H, I)
+    for c in (w13, w2):
+        c.qweight = _rand_i32(c.qweight.shape, g)
+        c.scales = (torch.rand(c.scales.shape, generator=g) * 0.02 + 1e-3).to(torch.float16)
+        c.qzeros = torch.full(c.qzeros.shape, 0x77777777, dtype=torch.int32)
+    ops = []
+    for c in (w13, w2):
+        parts = [kernels.gptq_to_op_layout(c.qweight[e], c.scales[e], c.qzeros[e]) for e in range(E)]
+        ops.append((torch.stack([p[0] for p in parts]).to(dev), torch.stack([p[1] for p in parts]).to(dev)))
+        c.qweight, c.scales, c.qzeros = c.qweight.to(dev), c.scales.to(dev), c.qzeros.to(dev)
+        c.post_load()
+    assert w13._zeros_op is None and w13._w_op.dtype == torch.uint8
+    x = synth.activations(T, H, seed=8).to(dev)
+    logits = synth.router_logits(T, E, seed=9).to(dev)
+    out = m.apply(w13, w2, x, router_logits=logits, topk_weights=None, topk_ids=None, top_k=k, renormalize=True,
+                  activation="silu", apply_router_weight_on_input=False)
+    ref = kernels.w4a8_moe(x, ops[0][0], ops[0][1], None, ops[1][0], ops[1][1], None, logits, k, True)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    # the EP shard kernel with a precomputed route is the same computation
+    tw, ti = kernels._moe_route(logits, k, True, E)
+    out_ep = m.ep_local(w13, w2, x, tw, ti, top_k=k, renormalize=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out_ep, out)
