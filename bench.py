@@ -154,7 +154,7 @@ def main() -> int:
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py: this build measures one MI355X; --gpus {args.gpus} (WORLD_SIZE={world}) is not run. "
-              f"Multi-GPU sharding of the path is described in DESIGN.md.", file=sys.stderr)
+              f"Every GPU box of this build has one GPU; a figure at several GPUs is not measured.", file=sys.stderr)
         return 2
 
     import torch
