@@ -16,6 +16,7 @@ int launch_gemv(GemmArgs p, int64_t row_blocks, bool quant_src, hipStream_t stre
 bool gemv_can_fuse_quant(const GemmArgs& p, int64_t row_blocks);
 size_t gemv_workspace_bytes(int64_t M, int64_t N, int64_t K, int grouped, int64_t row_blocks);
 int launch_prefill(const GemmArgs& p, int64_t rows_to_cover, int bm_rows, hipStream_t stream);
+int launch_prefill_lds(const GemmArgs& p, int64_t rows_to_cover, int bm_rows, hipStream_t stream);
 int launch_moe_route(const void* logits, int dtype, int64_t T, int E, int top_k, int renorm, float* tw,
                      int32_t* ids, hipStream_t stream);
 int launch_moe_align(const int32_t* ids, int64_t numel, int E, int bm, int64_t P, int32_t* sorted_ids,
@@ -141,7 +142,10 @@ static int run_dense(const char* who, GemmArgs& p, int kernel, hipStream_t strea
   char what[96];
   snprintf(what, sizeof what, "%s(%s)", who, decode ? "decode" : "prefill");
   if (decode) return hip_status(launch_gemv(p, (p.M + 15) / 16, false, stream), what);
-  return hip_status(launch_prefill(p, p.M, 128, stream), what);
+  // LDS-staged kernel for int4 groups of 128+ and MXFP4; the per-wave kernel for the rest
+  int rc = launch_prefill_lds(p, p.M, 0, stream);
+  if (rc == kErrUnsupported) rc = launch_prefill(p, p.M, 128, stream);
+  return hip_status(rc, what);
 }
 
 static int64_t round256(int64_t b) { return (b + 255) / 256 * 256; }
@@ -274,7 +278,9 @@ int w4a8_moe_gemm(const uint8_t* a_fp8, int64_t lda, const float* a_scales, int 
     return hip_status(launch_gemv(p, rb, false, (hipStream_t)stream), "w4a8_moe_gemm(decode)");
   }
   const int bm_rows = block_m % 128 == 0 ? 128 : 64;
-  return hip_status(launch_prefill(p, nblk * block_m, bm_rows, (hipStream_t)stream), "w4a8_moe_gemm(prefill)");
+  rc = launch_prefill_lds(p, nblk * block_m, bm_rows, (hipStream_t)stream);
+  if (rc == kErrUnsupported) rc = launch_prefill(p, nblk * block_m, bm_rows, (hipStream_t)stream);
+  return hip_status(rc, "w4a8_moe_gemm(prefill)");
 }
 
 int w4a8_moe_combine(const float* y, int64_t ldy, const int32_t* inv_pos, const float* topk_w, int64_t T, int top_k,

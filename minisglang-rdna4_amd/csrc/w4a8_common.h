@@ -129,6 +129,14 @@ __device__ __forceinline__ uint4 bload128(BufRsrc r, uint32_t voff, uint32_t sof
   const v4u v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
   return make_uint4(v.x, v.y, v.z, v.w);
 }
+__device__ __forceinline__ v4u bload128v(BufRsrc r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+}
+__device__ __forceinline__ uint2 bload64(BufRsrc r, uint32_t voff, uint32_t soff) {
+  typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+  const v2u v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
+  return make_uint2(v.x, v.y);
+}
 // streaming (non-temporal) variant for data read exactly once, such as weight tiles
 __device__ __forceinline__ uint4 bload128_nt(BufRsrc r, uint32_t voff, uint32_t soff) {
   const v4u v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 2);
