@@ -66,8 +66,11 @@ struct LdsStage {
   static constexpr int kBytes = kA + kB + kS + kZ;
 };
 
-template <int WM, int WN, int RB, int NSB, int MODE>
-__global__ void __launch_bounds__(WM * WN * 64) gemm_lds_kernel(const GemmArgs p) {
+// WPE: waves per SIMD the register budget is sized for (2: 256 registers per wave; 1: 512, for
+// the large wave tiles whose accumulators live in AGPRs).
+template <int WM, int WN, int RB, int NSB, int MODE, int WPE>
+__global__ void __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
+gemm_lds_kernel(const GemmArgs p) {
   constexpr int T = WM * WN * 64;
   constexpr int BM = WM * RB * 16, BN = WN * NSB * 16;
   constexpr int NSTRIP = BN / 16;
@@ -220,59 +223,61 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_lds_kernel(const GemmArgs p
   asm volatile("" : "+v"(oa), "+v"(ob), "+v"(os), "+v"(oz));
   const int zsh = 4 * (lane & 7);
 
-  // MFMA work of one K step from LDS stage `cur`
+  // MFMA work of one K step from LDS stage `cur`. Operands are read one strip (or row block) ahead
+  // of the MFMAs that use them, so a wave's LDS latency hides under its own MFMAs.
   auto compute = [&](int cur) __attribute__((always_inline)) {
     const unsigned char* st = lds + cur * S::kBytes;
+    if (MODE == kPE8M0) {
+      // all of the wave's fp4 strips and scale bytes (4 VGPRs + 1 per strip), then row blocks
+      uint4 braw[NSB];
+      int sbyte[NSB];
+#pragma unroll
+      for (int j = 0; j < NSB; ++j) {
+        braw[j] = *reinterpret_cast<const uint4*>(st + ob + j * 1024);
+        sbyte[j] = (int)st[os + j * 64];
+      }
+      v8i a0 = lds_operand(st + oa, 0);
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        v8i a1;
+        if (rb + 1 < RB) a1 = lds_operand(st + oa + (rb + 1) * 2048, 0);
+        __builtin_amdgcn_sched_barrier(0);  // the read stays ahead of this row block's MFMAs
+#pragma unroll
+        for (int j = 0; j < NSB; ++j) acc[rb][j] = mfma_f8f4_sb(a0, fp4_operand(braw[j]), acc[rb][j], sbyte[j]);
+        if (rb + 1 < RB) a0 = a1;
+      }
+      return;
+    }
     v8i a[RB];
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) a[rb] = lds_operand(st + oa + rb * 2048, 0);
     v4f pre[RB];
-    if (MODE == kPSym) {
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb) pre[rb] = mfma_f8f8(a[rb], splat8(0xB0B0B0B0u), zero4);  // -R/2
-    } else if (MODE == kPAsym) {
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb) pre[rb] = mfma_f8f8(a[rb], splat8(kE4M3Half4), zero4);  // +R/2
-    }
-    if (MODE == kPE8M0) {
-#pragma unroll
-      for (int j = 0; j < NSB; ++j) {
-        const uint4 raw = *reinterpret_cast<const uint4*>(st + ob + j * 1024);
-        const int sbyte = (int)st[os + j * 64];
-        const v8i b = fp4_operand(raw);
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) acc[rb][j] = mfma_f8f4_sb(a[rb], b, acc[rb][j], sbyte);
-      }
-    }
-    if (MODE != kPE8M0) {
-      // int4: each strip's MFMA partials are scaled into the accumulators while the next strip's
-      // MFMAs run, so only two strips of partials are live at a time
+    for (int rb = 0; rb < RB; ++rb)  // symmetric: -R/2; zero points: +R/2
+      pre[rb] = mfma_f8f8(a[rb], splat8(MODE == kPSym ? 0xB0B0B0B0u : kE4M3Half4), zero4);
+    if (MODE == kPAsym) {
+      // zero points: acc += s * (C + (15 - 2z) R/2); strip j's MFMAs run while strip j-1's
+      // partials are scaled in (operands read at use: no registers to spare for a lookahead at
+      // two waves per SIMD)
       v4f cp[RB];
-      float scp = 0.f, cfp = -1.f;
+      float scp = 0.f, cfp = 0.f;
 #pragma unroll
       for (int j = 0; j <= NSB; ++j) {
         v4f cj[RB];
-        float scj = 0.f, cfj = -1.f;
+        float scj = 0.f, cfj = 0.f;
         if (j < NSB) {
           const v8i b = lds_operand(st + ob + j * 2048, 0);
           scj = f16_to_f32(*reinterpret_cast<const uint16_t*>(st + os + j * 32));
-          if (MODE == kPAsym) {
-            const uint32_t zw = *reinterpret_cast<const uint32_t*>(st + oz + j * 8);
-            cfj = 15.0f - 2.0f * (float)((zw >> zsh) & 15u);
-          }
+          const uint32_t zw = *reinterpret_cast<const uint32_t*>(st + oz + j * 8);
+          cfj = 15.0f - 2.0f * (float)((zw >> zsh) & 15u);
 #pragma unroll
-          for (int rb = 0; rb < RB; ++rb) cj[rb] = mfma_f8f8(a[rb], b, MODE == kPSym ? pre[rb] : zero4);
+          for (int rb = 0; rb < RB; ++rb) cj[rb] = mfma_f8f8(a[rb], b, zero4);
         }
         if (j > 0) {
 #pragma unroll
           for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              if (MODE == kPSym)
-                acc[rb][j - 1][r] += scp * cp[rb][r];
-              else
-                acc[rb][j - 1][r] += scp * (cp[rb][r] + cfp * pre[rb][r]);
-            }
+            for (int r = 0; r < 4; ++r) acc[rb][j - 1][r] += scp * (cp[rb][r] + cfp * pre[rb][r]);
         }
         if (j < NSB) {
 #pragma unroll
@@ -280,6 +285,40 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_lds_kernel(const GemmArgs p
           scp = scj;
           cfp = cfj;
         }
+      }
+      return;
+    }
+    // symmetric: strip j's MFMAs run while strip j+1's operand is read and strip j-1's partials
+    // are scaled into the accumulators
+    v8i bn = lds_operand(st + ob, 0);
+    float scn = f16_to_f32(*reinterpret_cast<const uint16_t*>(st + os));
+    v4f cp[RB];
+    float scp = 0.f;
+#pragma unroll
+    for (int j = 0; j <= NSB; ++j) {
+      v4f cj[RB];
+      float scj = 0.f;
+      if (j < NSB) {
+        const v8i b = bn;
+        scj = scn;
+        if (j + 1 < NSB) {
+          bn = lds_operand(st + ob + (j + 1) * 2048, 0);
+          scn = f16_to_f32(*reinterpret_cast<const uint16_t*>(st + os + (j + 1) * 32));
+        }
+        __builtin_amdgcn_sched_barrier(0);  // the reads stay ahead of this strip's MFMAs
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) cj[rb] = mfma_f8f8(a[rb], b, pre[rb]);
+      }
+      if (j > 0) {
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[rb][j - 1][r] += scp * cp[rb][r];
+      }
+      if (j < NSB) {
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) cp[rb] = cj[rb];
+        scp = scj;
       }
     }
   };
@@ -363,11 +402,11 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_lds_kernel(const GemmArgs p
   }
 }
 
-template <int WM, int WN, int RB, int NSB, int MODE>
+template <int WM, int WN, int RB, int NSB, int MODE, int WPE>
 static void launch_lds_one(const GemmArgs& p, dim3 grid, dim3 block, hipStream_t stream) {
   constexpr int BM = WM * RB * 16, BN = WN * NSB * 16;
   constexpr size_t lds = 2 * (size_t)LdsStage<BM, BN, MODE>::kBytes;
-  auto kern = gemm_lds_kernel<WM, WN, RB, NSB, MODE>;
+  auto kern = gemm_lds_kernel<WM, WN, RB, NSB, MODE, WPE>;
   // dynamic LDS above 64 KiB must be allowed per kernel, once
   static const hipError_t attr =
       hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -375,16 +414,16 @@ static void launch_lds_one(const GemmArgs& p, dim3 grid, dim3 block, hipStream_t
   hipLaunchKernelGGL(kern, grid, block, lds, stream, p);
 }
 
-template <int WM, int WN, int RB, int NSB>
+template <int WM, int WN, int RB, int NSB, int WPE = 2>
 static int launch_lds_cfg(const GemmArgs& p, int mode, int64_t row_tiles, hipStream_t stream) {
   constexpr int BN = WN * NSB * 16;
   const int64_t ncols = p.silu ? p.N / 2 : p.N;
   const int64_t colw = p.silu ? BN / 2 : BN;
   const dim3 grid((unsigned)((ncols + colw - 1) / colw), (unsigned)row_tiles);
   const dim3 block(WM * WN * 64);
-  if (mode == kPSym) launch_lds_one<WM, WN, RB, NSB, kPSym>(p, grid, block, stream);
-  else if (mode == kPAsym) launch_lds_one<WM, WN, RB, NSB, kPAsym>(p, grid, block, stream);
-  else launch_lds_one<WM, WN, RB, NSB, kPE8M0>(p, grid, block, stream);
+  if (mode == kPSym) launch_lds_one<WM, WN, RB, NSB, kPSym, WPE>(p, grid, block, stream);
+  else if (mode == kPAsym) launch_lds_one<WM, WN, RB, NSB, kPAsym, WPE>(p, grid, block, stream);
+  else launch_lds_one<WM, WN, RB, NSB, kPE8M0, WPE>(p, grid, block, stream);
   return hipGetLastError() == hipSuccess ? kOk : kErrHip;
 }
 
