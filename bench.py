@@ -13,6 +13,11 @@ the largest shape (gate_up, M=1, one launch per call): algorithmic bytes per lau
 time from HIP events on the launch stream, against 8 TB/s. cpu_baseline is the reference's
 dequantize-then-matmul CPU path (oracle/baseline.py) on a bounded sample, rank 0 only.
 
+other_configs reports the remaining BASELINE configs through the same operator API: cfg1 (AWQ
+zero-point int4, M=16, K=2560, N=9728), cfg4 (MoE E=128 top-8 H=2048 I=768, T in {1,16,256,4096})
+and cfg5 (MXFP4 E8M0, K x N in {8192x28672, 28672x8192}, M in {1,16,4096}); GB/s against 8 TB/s
+for the decode sizes, TFLOPS against the 5 PFLOPS fp8 peak for the large ones.
+
 Modes for profiling runs (same committed file): --profile-kernel runs only the roofline loop,
 --copy-calib runs a plain device copy of known size (for scaling rocprofv3 byte counters).
 """
@@ -141,6 +146,112 @@ def prefill_leg(kernels, dev) -> dict:
     return out
 
 
+def _time_calls(calls, reps: int) -> float:
+    """Mean microseconds per call of `reps` calls cycling through `calls`, queued behind a GPU sleep
+    and bracketed by one event pair on the launching stream (kernels plus back-to-back gaps)."""
+    import torch
+
+    for c in calls[: min(len(calls), 3)]:
+        c()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(50_000_000)
+    a.record(stream)
+    for i in range(reps):
+        calls[i % len(calls)]()
+    b.record(stream)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1e3 / reps
+
+
+def _rand_words(shape, gen, dev):
+    import torch
+
+    return torch.randint(-2**31, 2**31 - 1, shape, generator=gen, device=dev, dtype=torch.int32)
+
+
+def _gbs(nbytes: int, us: float) -> dict:
+    g = nbytes / (us * 1e-6) / 1e9
+    return {"us": round(us, 2), "GB/s": round(g, 1), "frac_hbm_peak": round(g / HBM_PEAK_GBS, 4), "bytes": nbytes}
+
+
+def _tflops(flops: float, us: float) -> dict:
+    t = flops / (us * 1e-6) / 1e12
+    return {"us": round(us, 1), "TFLOPS": round(t, 1), "frac_fp8_peak": round(t / FP8_PEAK_TFLOPS, 4)}
+
+
+def configs_leg(kernels, dev) -> dict:
+    """The other BASELINE configs through the product's operator API, weights rotated over more
+    than twice the 256 MB MALL for the bandwidth-bound cases: cfg1 (AWQ zero-point int4 g128,
+    M=16, K=2560, N=9728), cfg4 (MoE E=128 top-8 H=2048 I=768, int4 g128 fp16 scales, T in
+    {1,16,256,4096}) and cfg5 (MXFP4 E8M0 block-32 at K=8192,N=28672 and K=28672,N=8192, M in
+    {1,16,4096}). Bytes and FLOPs count the algorithmic traffic (codes, scales, zero words,
+    bf16 activations in and out; MoE: the distinct experts the route selected)."""
+    import torch
+
+    out = {}
+    gen = torch.Generator(device=dev).manual_seed(11)
+    # cfg1: AWQ dense decode
+    M, K, N, g = 16, 2560, 9728, 128
+    copies = []
+    for _ in range(40):
+        t = kernels.repack_w4(_rand_words((N, K // 8), gen, dev))
+        sc = (torch.randn(K // g, N, generator=gen, device=dev).abs() * 0.02 + 1e-4).to(torch.float16)
+        z = _rand_words((K // g, N // 8), gen, dev)
+        copies.append((t, sc, z))
+    x = make_x(M, K, 101, dev)
+    us = _time_calls([lambda c=c: kernels.w4a8_linear(x, c[0], c[1], c[2], g) for c in copies], 80)
+    nb = N * K // 2 + (K // g) * N * 2 + (K // g) * N // 2 + M * K * 2 + M * N * 2
+    out["cfg1_awq_M16_K2560_N9728"] = _gbs(nb, us)
+    del copies
+    # cfg5: MXFP4
+    for (K, N) in [(8192, 28672), (28672, 8192)]:
+        copies = []
+        for _ in range(5):
+            t = kernels.repack_w4(_rand_words((N, K // 8), gen, dev), weight_is_e2m1=True)
+            sc = torch.randint(119, 128, (K // 32, N), generator=gen, device=dev, dtype=torch.int32).to(torch.uint8)
+            copies.append((t, sc))
+        for M in (1, 16):
+            x = make_x(M, K, 200 + M, dev)
+            us = _time_calls([lambda c=c: kernels.w4a8_linear(x, c[0], c[1], None, 32, weight_is_e2m1=True)
+                              for c in copies], 40)
+            nb = N * K // 2 + (K // 32) * N + M * K * 2 + M * N * 2
+            out[f"cfg5_mxfp4_M{M}_K{K}_N{N}"] = _gbs(nb, us)
+        M = 4096
+        x = make_x(M, K, 300, dev)
+        q, s = kernels.act_quant(x)
+        c = copies[0]
+        us = _time_calls([lambda: kernels.w4a8_linear(x, c[0], c[1], None, 32, weight_is_e2m1=True, x_fp8=q,
+                                                      act_scales=s)], 5)
+        out[f"cfg5_mxfp4_M{M}_K{K}_N{N}"] = _tflops(2.0 * M * N * K, us)
+        del copies
+    # cfg4: MoE
+    E, k, H, I, g = 128, 8, 2048, 768, 128
+    layers = []
+    for _ in range(2):
+        w13 = kernels.repack_w4(_rand_words((E, 2 * I, H // 8), gen, dev))
+        s13 = (torch.randn(E, H // g, 2 * I, generator=gen, device=dev).abs() * 0.02 + 1e-4).to(torch.float16)
+        w2 = kernels.repack_w4(_rand_words((E, H, I // 8), gen, dev))
+        s2 = (torch.randn(E, I // g, H, generator=gen, device=dev).abs() * 0.02 + 1e-4).to(torch.float16)
+        layers.append((w13, s13, w2, s2))
+    per_expert = 2 * I * H // 2 + (H // g) * 2 * I * 2 + H * I // 2 + (I // g) * H * 2
+    for T in (1, 16, 256, 4096):
+        x = make_x(T, H, 400 + T, dev)
+        logits = torch.randn(T, E, generator=gen, device=dev).to(torch.bfloat16)
+        distinct = int(torch.topk(logits.float(), k, dim=-1).indices.unique().numel())
+        calls = [lambda L=L: kernels.w4a8_moe(x, L[0], L[1], None, L[2], L[3], None, logits, k, True) for L in layers]
+        us = _time_calls(calls, 20 if T < 4096 else 5)
+        if T < 4096:
+            r = _gbs(distinct * per_expert + 2 * T * H * 2, us)
+        else:
+            r = _tflops(2.0 * T * k * (H * 2 * I + I * H), us)
+        r["distinct_experts"] = distinct
+        out[f"cfg4_moe_T{T}"] = r
+    del layers
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -150,6 +261,7 @@ def main() -> int:
     ap.add_argument("--copy-calib", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-configs", action="store_true")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -222,6 +334,7 @@ def main() -> int:
     # shape; the roofline leg covers the dominant shape)
     roof = roofline_leg(kernels, dev)
     prefill = None if args.no_prefill else prefill_leg(kernels, dev)
+    others = None if args.no_configs else configs_leg(kernels, dev)
     cpu = None if args.no_cpu_baseline else cpu_baseline_leg()
 
     line = {
@@ -251,6 +364,7 @@ def main() -> int:
         "roofline": roof,
         "cpu_baseline": cpu,
         "prefill_config3": prefill,
+        "other_configs": others,
     }
     print(json.dumps(line))
     return 0
