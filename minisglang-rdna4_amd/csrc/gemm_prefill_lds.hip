@@ -22,49 +22,9 @@
 #include <cstdlib>
 #include <type_traits>
 
-#include "gemm_args.h"
+#include "prefill.h"
 
 namespace w4a8 {
-
-constexpr int kPSym = 0, kPAsym = 1, kPE8M0 = 2;
-
-__device__ __forceinline__ bool lrow_source(const GemmArgs& p, int64_t r, int64_t& ar) {
-  if (!p.sorted_ids) {
-    ar = r;
-    return r < p.M;
-  }
-  if (r >= p.M || r >= (int64_t)(*p.ntp)) return false;
-  const int64_t slot = p.sorted_ids[r];
-  if (slot >= p.num_slots) return false;
-  ar = p.a_by_token ? slot / p.top_k : r;
-  return true;
-}
-
-__device__ __forceinline__ float lsilu_mul(float gate, float up, int dt) {
-  // tools/w4a8_gemm_silu_parity.py:52-54: round to dtype, silu in f32, round, multiply in dtype
-  const float g = from_dtype(to_dtype(gate, dt), dt);
-  const float u = from_dtype(to_dtype(up, dt), dt);
-  const float sg = g / (1.0f + expf(-g));
-  return from_dtype(to_dtype(sg, dt), dt) * u;
-}
-
-__device__ __forceinline__ v8i lds_operand(const unsigned char* base, int lane) {
-  const uint4 lo = *reinterpret_cast<const uint4*>(base + lane * 16);
-  const uint4 hi = *reinterpret_cast<const uint4*>(base + 1024 + lane * 16);
-  v8i a;
-  a[0] = (int)lo.x; a[1] = (int)lo.y; a[2] = (int)lo.z; a[3] = (int)lo.w;
-  a[4] = (int)hi.x; a[5] = (int)hi.y; a[6] = (int)hi.z; a[7] = (int)hi.w;
-  return a;
-}
-
-template <int BM, int BN, int MODE>
-struct LdsStage {
-  static constexpr int kA = BM * 128;                          // fp8 operand order
-  static constexpr int kB = MODE == kPE8M0 ? BN * 64 : BN * 128;  // fp4 bytes, or unpacked fp8
-  static constexpr int kS = MODE == kPE8M0 ? BN * 4 : BN * 2;  // E8M0 [strip][lane] | fp16 [strip][16]
-  static constexpr int kZ = MODE == kPAsym ? BN / 2 : 0;       // zero words [strip][2]
-  static constexpr int kBytes = kA + kB + kS + kZ;
-};
 
 // WPE: waves per SIMD the register budget is sized for (2: 256 registers per wave; 1: 512, for
 // the large wave tiles whose accumulators live in AGPRs).
@@ -431,6 +391,9 @@ static int launch_lds_cfg(const GemmArgs& p, int mode, int64_t row_tiles, hipStr
 // per-wave kernel). bm_rows: rows per workgroup the caller requires (grouped: divides the align
 // block; 0 for dense).
 int launch_prefill_lds(const GemmArgs& p, int64_t rows_to_cover, int bm_rows, hipStream_t stream) {
+  // the DMA-staged pipeline first (three stages, A by LDS-DMA); this kernel covers what it leaves
+  const int rc = launch_prefill_dma(p, rows_to_cover, bm_rows, stream);
+  if (rc != kErrUnsupported) return rc;
   int mode;
   if (p.wfmt == kInt4 && p.sfmt == kScaleF16 && p.group % kTileK == 0)
     mode = p.zeros ? kPAsym : kPSym;
@@ -444,8 +407,8 @@ int launch_prefill_lds(const GemmArgs& p, int64_t rows_to_cover, int bm_rows, hi
   if (p.sorted_ids && bm_rows != 64 && bm_rows != 128) return kErrUnsupported;
   // 32-bit offsets within one matrix
   if ((int64_t)p.N * p.KT * 64 >= (int64_t)1 << 31) return kErrUnsupported;
-  if (bm_rows == 64) return launch_lds_cfg<1, 2, 4, 4>(p, mode, (rows_to_cover + 63) / 64, stream);
-  if (bm_rows == 128) return launch_lds_cfg<2, 2, 4, 4>(p, mode, (rows_to_cover + 127) / 128, stream);
+  if (bm_rows == 64) return launch_lds_cfg<2, 4, 2, 2>(p, mode, (rows_to_cover + 63) / 64, stream);
+  if (bm_rows == 128) return launch_lds_cfg<4, 2, 2, 4>(p, mode, (rows_to_cover + 127) / 128, stream);
   // dense: 256 x 128 tiles on 8 waves (two waves per SIMD hide each other's LDS and barrier
   // waits; measured faster than 128 x 128 on 4 waves for every format).
   // W4A8_PREFILL_ROWS=128|256 overrides the choice (tuning).
@@ -454,7 +417,7 @@ int launch_prefill_lds(const GemmArgs& p, int64_t rows_to_cover, int bm_rows, hi
     return e ? atoi(e) : 0;
   }();
   const int rows = forced == 128 ? 128 : 256;
-  if (rows == 128) return launch_lds_cfg<2, 2, 4, 4>(p, mode, (rows_to_cover + 127) / 128, stream);
+  if (rows == 128) return launch_lds_cfg<4, 2, 2, 4>(p, mode, (rows_to_cover + 127) / 128, stream);
   return launch_lds_cfg<4, 2, 4, 4>(p, mode, (rows_to_cover + 255) / 256, stream);
 }
 
