@@ -94,6 +94,16 @@ int w4a8_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, c
 int w4a8_moe_route(const void* logits, int logits_dtype, int64_t T, int64_t E, int top_k, int renormalize,
                    float* topk_w, int32_t* topk_ids, void* stream);
 
+/* Route + align in one call: replaces moe_hip.moe_route_align (python/minisgl/quant/kernels.py:423-447),
+ * with the outputs of w4a8_moe_route and w4a8_moe_align (numel = T*top_k). When x is non-NULL it also
+ * quantizes x (T, K) per token into x_fp8 / x_scales, as w4a8_act_quant does (the act-quant the grouped
+ * gemm1 needs, kernels.py:1703-1712). Up to 256 slots (T*top_k) run as a single launch: one workgroup
+ * routes and aligns while the others quantize the token rows. */
+int w4a8_moe_route_align(const void* logits, int logits_dtype, int64_t T, int64_t E, int top_k, int renormalize,
+                         int block_m, int64_t P, float* topk_w, int32_t* topk_ids, int32_t* sorted_ids,
+                         int32_t* expert_ids, int32_t* ntp, int32_t* inv_pos, const void* x, int x_dtype, int64_t K,
+                         int64_t ldx, uint8_t* x_fp8, int64_t ldq, float* x_scales, void* stream);
+
 /* Padded capacity numel + (E+1)*(block_m-1) of sorted_ids (python/minisgl/moe/fused.py:94). */
 int64_t w4a8_moe_padded_capacity(int64_t numel, int64_t E, int block_m);
 
@@ -119,7 +129,8 @@ int w4a8_moe_gemm(const uint8_t* a_fp8, int64_t lda, const float* a_scales, int 
                   const int32_t* zeros, int wfmt, int64_t group_size, void* out, int out_dtype, int64_t ldo, int silu,
                   void* workspace, int64_t workspace_bytes, int kernel, void* stream);
 
-/* Top-k weighted combine: out[t] = sum_j topk_w[t, j] * y[inv_pos[t*top_k + j]] in f32.
+/* Top-k weighted combine: out[t] = sum_j topk_w[t, j] * y[inv_pos[t*top_k + j]] in f32 (H and ldy
+ * multiples of 4; y 16-byte aligned, out 8-byte (16-byte for f32) aligned).
  * Replaces fp8_wmma.mmq_fp8_moe_gather_reduce (python/minisgl/quant/kernels.py:876-882). */
 int w4a8_moe_combine(const float* y, int64_t ldy, const int32_t* inv_pos, const float* topk_w, int64_t T, int top_k,
                      int64_t H, void* out, int out_dtype, void* stream);

@@ -23,6 +23,11 @@ int launch_moe_align(const int32_t* ids, int64_t numel, int E, int bm, int64_t P
                      int32_t* expert_ids, int32_t* ntp, int32_t* inv_pos, hipStream_t stream);
 int launch_moe_combine(const float* y, int64_t ldy, const int32_t* inv_pos, const float* tw, int64_t T,
                        int top_k, int64_t H, void* out, int dtype, hipStream_t stream);
+bool moe_prep_fits(int64_t T, int top_k);
+int launch_moe_prep(const void* logits, int ldtype, int64_t T, int E, int top_k, int renorm, float* tw,
+                    int32_t* ids, int bm, int64_t P, int32_t* sorted_ids, int32_t* expert_ids, int32_t* ntp,
+                    int32_t* inv_pos, const void* x, int xdtype, int64_t K, int64_t ldx, uint8_t* xq, int64_t ldq,
+                    float* xs, hipStream_t stream);
 }  // namespace w4a8
 
 using namespace w4a8;
@@ -204,14 +209,55 @@ int w4a8_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, c
   return run_dense("w4a8_linear", p, kernel, st);
 }
 
+static int check_route(const char* who, int logits_dtype, int64_t E, int top_k) {
+  if (logits_dtype != kBF16 && logits_dtype != kF16 && logits_dtype != kF32)
+    return fail(kErrInvalid, "%s: logits must be bf16, fp16 or f32", who);
+  if (E <= 0 || E > 512) return fail(kErrUnsupported, "%s: num_experts=%lld outside [1, 512]", who, (long long)E);
+  if (top_k <= 0 || top_k > E || top_k > 64) return fail(kErrInvalid, "%s: top_k=%d invalid for E=%lld", who, top_k, (long long)E);
+  return kOk;
+}
+
+static int check_align(const char* who, int64_t numel, int64_t E, int block_m, int64_t P) {
+  if (E <= 0 || E > 512) return fail(kErrUnsupported, "%s: num_experts=%lld outside [1, 512]", who, (long long)E);
+  if (block_m <= 0 || block_m % 16) return fail(kErrInvalid, "%s: block_m=%d must be a positive multiple of 16", who, block_m);
+  if (P < numel + (E + 1) * (block_m - 1))
+    return fail(kErrInvalid, "%s: capacity P=%lld < numel + (E+1)*(block_m-1)", who, (long long)P);
+  if (numel > 0x7fffffff) return fail(kErrInvalid, "%s: too many slots", who);
+  return kOk;
+}
+
 int w4a8_moe_route(const void* logits, int logits_dtype, int64_t T, int64_t E, int top_k, int renormalize,
                    float* topk_w, int32_t* topk_ids, void* stream) {
-  if (logits_dtype != kBF16 && logits_dtype != kF16 && logits_dtype != kF32)
-    return fail(kErrInvalid, "moe_route: logits must be bf16, fp16 or f32");
-  if (E <= 0 || E > 512) return fail(kErrUnsupported, "moe_route: num_experts=%lld outside [1, 512]", (long long)E);
-  if (top_k <= 0 || top_k > E || top_k > 64) return fail(kErrInvalid, "moe_route: top_k=%d invalid for E=%lld", top_k, (long long)E);
+  if (int rc = check_route("moe_route", logits_dtype, E, top_k)) return rc;
   return hip_status(launch_moe_route(logits, logits_dtype, T, (int)E, top_k, renormalize, topk_w, topk_ids,
                                      (hipStream_t)stream), "moe_route");
+}
+
+int w4a8_moe_route_align(const void* logits, int logits_dtype, int64_t T, int64_t E, int top_k, int renormalize,
+                         int block_m, int64_t P, float* topk_w, int32_t* topk_ids, int32_t* sorted_ids,
+                         int32_t* expert_ids, int32_t* ntp, int32_t* inv_pos, const void* x, int x_dtype, int64_t K,
+                         int64_t ldx, uint8_t* x_fp8, int64_t ldq, float* x_scales, void* stream) {
+  if (int rc = check_route("moe_route_align", logits_dtype, E, top_k)) return rc;
+  if (T < 0) return fail(kErrInvalid, "moe_route_align: T=%lld negative", (long long)T);
+  if (int rc = check_align("moe_route_align", T * top_k, E, block_m, P)) return rc;
+  if (x) {
+    if (x_dtype != kBF16 && x_dtype != kF16) return fail(kErrInvalid, "moe_route_align: x must be bf16 or fp16");
+    if (K <= 0 || K % 8) return fail(kErrInvalid, "moe_route_align: K=%lld must be a positive multiple of 8", (long long)K);
+    if (ldx < K || ldx % 8 || ldq < K || ldq % 8)
+      return fail(kErrInvalid, "moe_route_align: row strides must be >= K and multiples of 8 (ldx=%lld ldq=%lld)",
+                  (long long)ldx, (long long)ldq);
+    if (!aligned16(x) || !aligned16(x_fp8) || !x_scales)
+      return fail(kErrInvalid, "moe_route_align: x and x_fp8 must be 16-byte aligned and x_scales given");
+  }
+  const hipStream_t st = (hipStream_t)stream;
+  if (moe_prep_fits(T, top_k))
+    return hip_status(launch_moe_prep(logits, logits_dtype, T, (int)E, top_k, renormalize, topk_w, topk_ids, block_m, P,
+                                      sorted_ids, expert_ids, ntp, inv_pos, x, x_dtype, K, ldx, x_fp8, ldq, x_scales,
+                                      st), "moe_route_align");
+  int rc = launch_moe_route(logits, logits_dtype, T, (int)E, top_k, renormalize, topk_w, topk_ids, st);
+  if (!rc) rc = launch_moe_align(topk_ids, T * top_k, (int)E, block_m, P, sorted_ids, expert_ids, ntp, inv_pos, st);
+  if (!rc && x) rc = launch_act_quant(x, x_dtype, T, K, ldx, x_fp8, ldq, x_scales, nullptr, st);
+  return hip_status(rc, "moe_route_align");
 }
 
 int64_t w4a8_moe_padded_capacity(int64_t numel, int64_t E, int block_m) {
@@ -220,11 +266,7 @@ int64_t w4a8_moe_padded_capacity(int64_t numel, int64_t E, int block_m) {
 
 int w4a8_moe_align(const int32_t* topk_ids, int64_t numel, int64_t E, int block_m, int64_t P, int32_t* sorted_ids,
                    int32_t* expert_ids, int32_t* ntp, int32_t* inv_pos, void* stream) {
-  if (E <= 0 || E > 512) return fail(kErrUnsupported, "moe_align: num_experts=%lld outside [1, 512]", (long long)E);
-  if (block_m <= 0 || block_m % 16) return fail(kErrInvalid, "moe_align: block_m=%d must be a positive multiple of 16", block_m);
-  if (P < numel + (E + 1) * (block_m - 1))
-    return fail(kErrInvalid, "moe_align: capacity P=%lld < numel + (E+1)*(block_m-1)", (long long)P);
-  if (numel > 0x7fffffff) return fail(kErrInvalid, "moe_align: too many slots");
+  if (int rc = check_align("moe_align", numel, E, block_m, P)) return rc;
   return hip_status(launch_moe_align(topk_ids, numel, (int)E, block_m, P, sorted_ids, expert_ids, ntp, inv_pos,
                                      (hipStream_t)stream), "moe_align");
 }
@@ -287,6 +329,9 @@ int w4a8_moe_combine(const float* y, int64_t ldy, const int32_t* inv_pos, const 
                      int64_t H, void* out, int out_dtype, void* stream) {
   if (out_dtype != kBF16 && out_dtype != kF16 && out_dtype != kF32) return fail(kErrInvalid, "moe_combine: unknown dtype");
   if (ldy < H) return fail(kErrInvalid, "moe_combine: ldy < H");
+  if (H % 4 || ldy % 4 || !aligned16(y) || (reinterpret_cast<uintptr_t>(out) & (out_dtype == kF32 ? 15u : 7u)))
+    return fail(kErrInvalid, "moe_combine: H and ldy must be multiples of 4 with y 16-byte and out %d-byte aligned",
+                out_dtype == kF32 ? 16 : 8);
   return hip_status(launch_moe_combine(y, ldy, inv_pos, topk_w, T, top_k, H, out, out_dtype, (hipStream_t)stream),
                     "moe_combine");
 }

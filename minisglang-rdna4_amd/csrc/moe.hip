@@ -8,110 +8,171 @@
 // align: restates moe_align_block_size (python/minisgl/moe/fused.py:120-176): slots sorted by
 //   expert, stable in slot order, each expert padded to a multiple of block_m with the sentinel
 //   numel, per-block expert id (blocks past the end clamp to E-1), padded total ntp. A single
-//   workgroup builds it deterministically: an LDS histogram, a scan, then chunks of 1024 slots
-//   ranked with wave ballots (lanes holding the same expert) and per-wave counts in LDS.
+//   workgroup builds it deterministically: an LDS histogram, a scan, then chunks of slots ranked
+//   with per-wave lane masks and per-expert prefix sums over the waves.
 // combine: out[t] = sum_j tw[t,j] * y[pos(t,j)] in f32, j in slot order, cast to the activation
 //   dtype (mmq_fp8_moe_gather_reduce, kernels.py:876-882).
-#include "w4a8_common.h"
+#include "act_quant.h"
 
 namespace w4a8 {
 
 constexpr int kMaxExperts = 512;
-constexpr int kRouteMaxPerLane = kMaxExperts / 64;
 
 __device__ __forceinline__ float load_logit(const void* p, int dtype, int64_t i) {
   if (dtype == kF32) return reinterpret_cast<const float*>(p)[i];
   return from_dtype(reinterpret_cast<const uint16_t*>(p)[i], dtype);
 }
 
-__global__ void __launch_bounds__(256)
-moe_route_kernel(const void* __restrict__ logits, int dtype, int64_t T, int E, int top_k, int renorm,
-                 float* __restrict__ tw, int32_t* __restrict__ ids) {
+// (value, expert) argmax step against the DPP partner: larger logit, then lower expert index
+__device__ __forceinline__ bool beats(float ov, int oi, float bv, int bi) {
+  return (ov > bv) | ((ov == bv) & (oi < bi));  // non-short-circuit: selects, not branches
+}
+template <int CTRL>
+__device__ __forceinline__ void argmax_step(float& bv, int& bi) {
+  const float ov = dpp_f<CTRL>(bv);
+  const int oi = dpp_i<CTRL>(bi);
+  const bool take = beats(ov, oi, bv, bi);
+  bv = take ? ov : bv;
+  bi = take ? oi : bi;
+}
+
+// Route of token t by one wave (all 64 lanes active): lane l holds experts l + 64*i, i < PER.
+// Softmax over the f32-widened logits (max, then the sum of exp in a fixed tree order), top-k by
+// repeated wave argmax on the logits (which orders the experts exactly as the probabilities do;
+// ties keep the lower index), then renormalisation by the selected probabilities' sum, taken in
+// selection order, + 1e-8. Writes the k weights and ids to global memory and the ids to ids_s
+// (LDS, optional).
+template <int PER>
+__device__ __forceinline__ void route_token(const void* __restrict__ logits, int dtype, int64_t t, int E,
+                                            int top_k, int renorm, float* __restrict__ tw,
+                                            int32_t* __restrict__ ids, int32_t* ids_s) {
   const int lane = threadIdx.x & 63;
-  const int64_t t = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  if (t >= T) return;
-  float v[kRouteMaxPerLane];
+  // every load is issued before the first use, whatever the dtype
+  uint32_t raw[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int e = lane + 64 * i;
+    const int64_t idx = t * E + (e < E ? e : 0);
+    raw[i] = dtype == kF32 ? __float_as_uint(reinterpret_cast<const float*>(logits)[idx])
+                           : (uint32_t)reinterpret_cast<const uint16_t*>(logits)[idx];
+  }
+  float v[PER];
   float mx = -INFINITY;
 #pragma unroll
-  for (int i = 0; i < kRouteMaxPerLane; ++i) {
+  for (int i = 0; i < PER; ++i) {
     const int e = lane + 64 * i;
-    v[i] = e < E ? load_logit(logits, dtype, t * E + e) : -INFINITY;
+    v[i] = e >= E ? -INFINITY : dtype == kF32 ? __uint_as_float(raw[i]) : from_dtype((uint16_t)raw[i], dtype);
     mx = fmaxf(mx, v[i]);
   }
+  mx = wave_max(mx);
+  float part = 0.f;
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-  float sum = 0.f;
-#pragma unroll
-  for (int i = 0; i < kRouteMaxPerLane; ++i) {
-    const int e = lane + 64 * i;
-    if (e < E) sum += expf(v[i] - mx);
-  }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+  for (int i = 0; i < PER; ++i)
+    if (lane + 64 * i < E) part += expf(v[i] - mx);
+  const float sum = wave_sum(part);
 
   unsigned used = 0;  // bit i: expert lane + 64*i taken
-  float wsum = 0.f;
-  float myw = 0.f;
+  float myv = -INFINITY;
   int myid = 0;
   for (int j = 0; j < top_k; ++j) {
-    // lane-local best unused (largest logit, lowest index)
     float bv = -INFINITY;
     int bi = 0x7fffffff;
 #pragma unroll
-    for (int i = 0; i < kRouteMaxPerLane; ++i) {
+    for (int i = 0; i < PER; ++i) {
       const int e = lane + 64 * i;
-      if (e < E && !((used >> i) & 1u) && (v[i] > bv || (v[i] == bv && e < bi))) {
-        bv = v[i];
-        bi = e;
-      }
+      const bool take = (e < E) & !((used >> i) & 1u) & beats(v[i], e, bv, bi);
+      bv = take ? v[i] : bv;
+      bi = take ? e : bi;
     }
+    argmax_step<kDppXor1>(bv, bi);
+    argmax_step<kDppXor2>(bv, bi);
+    argmax_step<kDppHalfMirror>(bv, bi);
+    argmax_step<kDppRowMirror>(bv, bi);
+    // rows 0..3 each hold their argmax in every lane; combine them in scalar registers
+    float cv = lane_f(bv, 0);
+    int ci = __builtin_amdgcn_readlane(bi, 0);
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(bv, o, 64);
-      const int oi = __shfl_xor(bi, o, 64);
-      if (ov > bv || (ov == bv && oi < bi)) {
-        bv = ov;
-        bi = oi;
-      }
+    for (int r = 1; r < 4; ++r) {
+      const float ov = lane_f(bv, 16 * r);
+      const int oi = __builtin_amdgcn_readlane(bi, 16 * r);
+      const bool take = beats(ov, oi, cv, ci);
+      cv = take ? ov : cv;
+      ci = take ? oi : ci;
     }
+    bv = cv;
+    bi = ci;
     if ((bi & 63) == lane) used |= 1u << (bi >> 6);
-    const float p = expf(bv - mx) / sum;
-    wsum += p;
     if (lane == j) {
-      myw = p;
+      myv = bv;
       myid = bi;
     }
   }
+  const float p = lane < top_k ? expf(myv - mx) / sum : 0.f;
+  float wsum = 0.f;
+  for (int j = 0; j < top_k; ++j) wsum += lane_f(p, j);
   if (lane < top_k) {
-    tw[t * top_k + lane] = renorm ? myw / (wsum + 1e-8f) : myw;
+    tw[t * top_k + lane] = renorm ? p / (wsum + 1e-8f) : p;
     ids[t * top_k + lane] = myid;
+    if (ids_s) ids_s[t * top_k + lane] = myid;
   }
 }
 
-constexpr int kAlignThreads = 1024;
-constexpr int kAlignWaves = kAlignThreads / 64;
+template <int PER>
+__global__ void __launch_bounds__(256)
+moe_route_kernel(const void* __restrict__ logits, int dtype, int64_t T, int E, int top_k, int renorm,
+                 float* __restrict__ tw, int32_t* __restrict__ ids) {
+  const int64_t t = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (t >= T) return;  // whole waves leave together
+  route_token<PER>(logits, dtype, t, E, top_k, renorm, tw, ids, nullptr);
+}
 
-__global__ void __launch_bounds__(kAlignThreads)
-moe_align_kernel(const int32_t* __restrict__ ids, int64_t numel, int E, int bm, int64_t P,
-                 int32_t* __restrict__ sorted_ids, int32_t* __restrict__ expert_ids,
-                 int32_t* __restrict__ ntp_out, int32_t* __restrict__ inv_pos) {
-  __shared__ int cnt[kMaxExperts];
-  __shared__ int base[kMaxExperts];
-  __shared__ int wcount[kAlignWaves][kMaxExperts];
-  __shared__ int wsums[kAlignWaves];
+// Align of numel slots by one workgroup of NT threads (E <= EMAX): an LDS histogram, a scan of the
+// padded counts, then chunks of NT slots. In a chunk every wave marks its lanes in a per-wave,
+// per-expert 64-bit lane mask (LDS atomic OR): a lane's rank among the wave's lanes holding its
+// expert is the popcount of the mask below it, and per-expert prefix sums of the mask popcounts
+// over the waves give each wave's offset, so the order is stable in slot order. ids may point to
+// global memory or LDS. With HELD > 0 the histogram pass, which reads every id once with
+// independent loads, also keeps the first HELD ids in LDS as 16-bit values, so the chunk loop waits
+// on no global load. Every output element is written by exactly one thread (slots by the scatter,
+// padding and the tail by the fill), so no global store has to land before another: the barriers
+// only order LDS traffic and never drain the stores in flight.
+template <int NT, int EMAX, int HELD>
+__device__ __forceinline__ void align_block(const int32_t* ids, int64_t numel, int E, int bm, int64_t P,
+                                            int32_t* __restrict__ sorted_ids, int32_t* __restrict__ expert_ids,
+                                            int32_t* __restrict__ ntp_out, int32_t* __restrict__ inv_pos) {
+  constexpr int NW = NT / 64;
+  static_assert(NT >= EMAX, "one scan pass: a thread per expert");
+  __shared__ int cnt[EMAX];
+  __shared__ int base[EMAX];
+  __shared__ unsigned long long mask[NW][EMAX];
+  __shared__ int pre[NW][EMAX];
+  __shared__ int wsums[NW];
   __shared__ int total_s;
+  __shared__ uint16_t held[HELD > 0 ? HELD : 1];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  for (int e = tid; e < kMaxExperts; e += kAlignThreads) cnt[e] = 0;
-  for (int i = tid; i < kAlignWaves * kMaxExperts; i += kAlignThreads) (&wcount[0][0])[i] = 0;
-  __syncthreads();
-  for (int64_t i = tid; i < numel; i += kAlignThreads) {
-    const int e = ids[i];
-    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+  for (int e = tid; e < EMAX; e += NT) cnt[e] = 0;
+  for (int i = tid; i < NW * EMAX; i += NT) (&mask[0][0])[i] = 0ull;
+  lds_barrier();
+  // eight independent loads in flight per thread per batch
+  for (int64_t i0 = 0; i0 < numel; i0 += 8 * NT) {
+    int ev[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int64_t i = i0 + u * NT + tid;
+      ev[u] = i < numel ? ids[i] : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int64_t i = i0 + u * NT + tid;
+      int e = ev[u];
+      if (e < 0 || e >= E) e = -1;
+      if (HELD > 0 && i < HELD && i < numel) held[i] = (uint16_t)e;  // -1 is kept as 0xffff
+      if (e >= 0) atomicAdd(&cnt[e], 1);
+    }
   }
-  __syncthreads();
-  // exclusive scan of padded counts over experts (E <= 1024 = one element per thread)
-  int padded = 0;
-  if (tid < E) padded = (cnt[tid] + bm - 1) / bm * bm;
+  lds_barrier();
+  // exclusive scan of padded counts over experts (one expert per thread)
+  const int padded = tid < E ? (cnt[tid] + bm - 1) / bm * bm : 0;
   int incl = padded;
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
@@ -119,112 +180,223 @@ moe_align_kernel(const int32_t* __restrict__ ids, int64_t numel, int E, int bm, 
     if (lane >= o) incl += n;
   }
   if (lane == 63) wsums[wave] = incl;
-  __syncthreads();
+  lds_barrier();
   if (tid == 0) {
     int run = 0;
-    for (int w = 0; w < kAlignWaves; ++w) {
+    for (int w = 0; w < NW; ++w) {
       const int s = wsums[w];
       wsums[w] = run;
       run += s;
     }
     total_s = run;
   }
-  __syncthreads();
-  const int excl = incl - padded + wsums[wave];
-  if (tid < E) base[tid] = excl;
+  lds_barrier();
+  if (tid < E) base[tid] = incl - padded + wsums[wave];
   const int total = total_s;
-  __syncthreads();
-  // fill sentinel and block owners
-  for (int64_t i = tid; i < P; i += kAlignThreads) sorted_ids[i] = (int32_t)numel;
-  const int64_t nblocks = (P + bm - 1) / bm;
-  for (int64_t b = tid; b < nblocks; b += kAlignThreads) expert_ids[b] = E - 1;
-  __syncthreads();
+  lds_barrier();
+  // padding rows of each expert and the tail [ntp, P) hold the sentinel numel
+  for (int64_t x = tid; x < (int64_t)E * (bm - 1); x += NT) {
+    const int e = (int)(x / (bm - 1)), j = (int)(x - (int64_t)e * (bm - 1));
+    const int c = cnt[e];
+    if (c + j < (c + bm - 1) / bm * bm) sorted_ids[base[e] + c + j] = (int32_t)numel;
+  }
+  for (int64_t i = total + tid; i < P; i += NT) sorted_ids[i] = (int32_t)numel;
+  // block owners; blocks past the end clamp to E-1
   if (tid < E) {
     const int b0 = base[tid] / bm, nb = (cnt[tid] + bm - 1) / bm;
     for (int b = 0; b < nb; ++b) expert_ids[b0 + b] = tid;
   }
+  const int64_t nblocks = (P + bm - 1) / bm;
+  for (int64_t b = total / bm + tid; b < nblocks; b += NT) expert_ids[b] = E - 1;
   if (tid == 0) *ntp_out = total;
-  // stable scatter in chunks of kAlignThreads slots
-  for (int64_t c0 = 0; c0 < numel; c0 += kAlignThreads) {
+  // stable scatter in chunks of NT slots
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  for (int64_t c0 = 0; c0 < numel; c0 += NT) {
     const int64_t i = c0 + tid;
     int e = -1;
     if (i < numel) {
-      e = ids[i];
-      if (e < 0 || e >= E) e = -1;
+      if (HELD > 0 && i < HELD) {
+        const uint16_t h = held[i];
+        e = h == 0xffffu ? -1 : (int)h;
+      } else {
+        e = ids[i];
+        if (e >= E) e = -1;
+      }
     }
-    const int key = e < 0 ? 0x7ff : e;  // 11-bit key; invalid slots group together and are dropped
-    uint64_t peers = __ballot(1);
+    if (e >= 0) atomicOr(&mask[wave][e], 1ull << lane);
+    lds_barrier();
+    const uint64_t m = e >= 0 ? mask[wave][e] : 0ull;
+    if (tid < E) {
+      // per-expert offsets of the waves: exclusive prefix of the mask popcounts, from base
+      int run = base[tid];
 #pragma unroll
-    for (int b = 0; b < 11; ++b) {
-      const int bit = (key >> b) & 1;
-      const uint64_t bal = __ballot(bit);
-      peers &= bit ? bal : ~bal;
+      for (int w = 0; w < NW; ++w) {
+        const int c = __popcll(mask[w][tid]);
+        pre[w][tid] = run;
+        run += c;
+      }
+      base[tid] = run;
     }
-    const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-    const int rank = __popcll(peers & below);
-    const int leader = __ffsll((long long)peers) - 1;
-    if (e >= 0 && lane == leader) wcount[wave][e] = __popcll(peers);
-    if (e < 0 && i < numel && inv_pos) inv_pos[i] = -1;  // dropped slot: the combine skips it
-    __syncthreads();
+    lds_barrier();
     if (e >= 0) {
-      int off = base[e] + rank;
-      for (int w = 0; w < wave; ++w) off += wcount[w][e];
+      const int off = pre[wave][e] + __popcll(m & below);
       sorted_ids[off] = (int32_t)i;
       if (inv_pos) inv_pos[i] = off;
+      if (lane == __ffsll((long long)m) - 1) mask[wave][e] = 0ull;  // the wave's lowest lane clears
+    } else if (i < numel && inv_pos) {
+      inv_pos[i] = -1;  // dropped slot: the combine skips it
     }
-    __syncthreads();
-    if (tid < E) {
-      int add = 0;
-      for (int w = 0; w < kAlignWaves; ++w) {
-        add += wcount[w][tid];
-        wcount[w][tid] = 0;
-      }
-      base[tid] += add;
-    }
-    __syncthreads();
   }
 }
 
-__global__ void moe_combine_kernel(const float* __restrict__ y, int64_t ldy,
-                                   const int32_t* __restrict__ inv_pos, const float* __restrict__ tw,
-                                   int64_t T, int top_k, int64_t H, void* __restrict__ out, int dtype) {
-  const int64_t h = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+constexpr int kAlignHeld = 32768;  // slots whose ids the histogram pass keeps in LDS (64 KiB)
+
+// E <= 256: 1024 threads; E <= 512: 512 threads (the per-wave masks and offsets scale with both)
+template <int NT, int EMAX>
+__global__ void __launch_bounds__(NT)
+moe_align_kernel(const int32_t* __restrict__ ids, int64_t numel, int E, int bm, int64_t P,
+                 int32_t* __restrict__ sorted_ids, int32_t* __restrict__ expert_ids,
+                 int32_t* __restrict__ ntp_out, int32_t* __restrict__ inv_pos) {
+  align_block<NT, EMAX, kAlignHeld>(ids, numel, E, bm, P, sorted_ids, expert_ids, ntp_out, inv_pos);
+}
+
+// Small-batch route + align (+ per-token act quant of x) in one launch. Workgroup 0 routes the T
+// tokens (one wave per token, 16 at a time), keeping the ids in LDS, then aligns them; workgroups
+// 1..T each quantize one token row of x (quant_row, the act-quant kernel's arithmetic) in parallel
+// with it.
+constexpr int kPrepThreads = 1024;
+constexpr int kPrepMaxSlots = 256;
+
+template <int PER, int CPT>
+__global__ void __launch_bounds__(kPrepThreads)
+moe_prep_kernel(const void* __restrict__ logits, int ldtype, int64_t T, int E, int top_k, int renorm,
+                float* __restrict__ tw, int32_t* __restrict__ ids, int bm, int64_t P,
+                int32_t* __restrict__ sorted_ids, int32_t* __restrict__ expert_ids, int32_t* __restrict__ ntp,
+                int32_t* __restrict__ inv_pos, const uint16_t* __restrict__ x, int xdtype, int64_t K, int64_t ldx,
+                uint8_t* __restrict__ xq, int64_t ldq, float* __restrict__ xs) {
+  if (blockIdx.x > 0) {
+    __shared__ float red[kPrepThreads / 64];
+    const int64_t m = blockIdx.x - 1;
+    quant_row<CPT, kPrepThreads>(x + m * ldx, K, xdtype, xq + m * ldq, xs + m, red);
+    return;
+  }
+  __shared__ int32_t ids_s[kPrepMaxSlots];
+  for (int64_t t = threadIdx.x >> 6; t < T; t += kPrepThreads / 64)
+    route_token<PER>(logits, ldtype, t, E, top_k, renorm, tw, ids, ids_s);
+  __syncthreads();
+  align_block<kPrepThreads, 64 * PER, 0>(ids_s, T * top_k, E, bm, P, sorted_ids, expert_ids, ntp, inv_pos);
+}
+
+// Four channels per thread: 16-byte loads of y, one 8-byte (or 16-byte f32) store.
+__global__ void __launch_bounds__(256)
+moe_combine_kernel(const float* __restrict__ y, int64_t ldy, const int32_t* __restrict__ inv_pos,
+                   const float* __restrict__ tw, int64_t T, int top_k, int64_t H, void* __restrict__ out, int dtype) {
+  const int64_t h = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
   if (h >= H) return;
   for (int64_t t = blockIdx.y; t < T; t += gridDim.y) {
-    float acc = 0.f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int j = 0; j < top_k; ++j) {
       const int64_t pos = inv_pos[t * top_k + j];
-      if (pos >= 0) acc += tw[t * top_k + j] * y[pos * ldy + h];
+      if (pos >= 0) {
+        const float w = tw[t * top_k + j];
+        const float4 v = *reinterpret_cast<const float4*>(y + pos * ldy + h);
+        acc.x += w * v.x;
+        acc.y += w * v.y;
+        acc.z += w * v.z;
+        acc.w += w * v.w;
+      }
     }
-    if (dtype == kF32)
-      reinterpret_cast<float*>(out)[t * H + h] = acc;
-    else
-      reinterpret_cast<uint16_t*>(out)[t * H + h] = to_dtype(acc, dtype);
+    if (dtype == kF32) {
+      *reinterpret_cast<float4*>(reinterpret_cast<float*>(out) + t * H + h) = acc;
+    } else {
+      const uint32_t lo = (uint32_t)to_dtype(acc.x, dtype) | ((uint32_t)to_dtype(acc.y, dtype) << 16);
+      const uint32_t hi = (uint32_t)to_dtype(acc.z, dtype) | ((uint32_t)to_dtype(acc.w, dtype) << 16);
+      *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(out) + t * H + h) = make_uint2(lo, hi);
+    }
   }
 }
+
+template <template <int> class F, typename... A>
+static void with_per(int E, A... a) {
+  if (E <= 64) F<1>::run(a...);
+  else if (E <= 128) F<2>::run(a...);
+  else if (E <= 256) F<4>::run(a...);
+  else F<8>::run(a...);
+}
+
+template <int PER> struct RouteLaunch {
+  static void run(const void* logits, int dtype, int64_t T, int E, int top_k, int renorm, float* tw, int32_t* ids,
+                  hipStream_t stream) {
+    const int per_block = 4;
+    hipLaunchKernelGGL(moe_route_kernel<PER>, dim3((unsigned)((T + per_block - 1) / per_block)), dim3(per_block * 64),
+                       0, stream, logits, dtype, T, E, top_k, renorm, tw, ids);
+  }
+};
 
 int launch_moe_route(const void* logits, int dtype, int64_t T, int E, int top_k, int renorm, float* tw,
                      int32_t* ids, hipStream_t stream) {
   if (T <= 0) return kOk;
-  const int per_block = 4;
-  hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)((T + per_block - 1) / per_block)),
-                     dim3(per_block * 64), 0, stream, logits, dtype, T, E, top_k, renorm, tw, ids);
+  with_per<RouteLaunch>(E, logits, dtype, T, E, top_k, renorm, tw, ids, stream);
   return hipGetLastError() == hipSuccess ? kOk : kErrHip;
 }
 
 int launch_moe_align(const int32_t* ids, int64_t numel, int E, int bm, int64_t P, int32_t* sorted_ids,
                      int32_t* expert_ids, int32_t* ntp, int32_t* inv_pos, hipStream_t stream) {
-  hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kAlignThreads), 0, stream, ids, numel, E, bm, P,
-                     sorted_ids, expert_ids, ntp, inv_pos);
+  if (E <= 256)
+    hipLaunchKernelGGL((moe_align_kernel<1024, 256>), dim3(1), dim3(1024), 0, stream, ids, numel, E, bm, P, sorted_ids,
+                       expert_ids, ntp, inv_pos);
+  else
+    hipLaunchKernelGGL((moe_align_kernel<512, 512>), dim3(1), dim3(512), 0, stream, ids, numel, E, bm, P, sorted_ids,
+                       expert_ids, ntp, inv_pos);
+  return hipGetLastError() == hipSuccess ? kOk : kErrHip;
+}
+
+template <int PER> struct PrepLaunch {
+  template <int CPT>
+  static void go(dim3 grid, hipStream_t stream, const void* logits, int ldtype, int64_t T, int E, int top_k,
+                 int renorm, float* tw, int32_t* ids, int bm, int64_t P, int32_t* sorted_ids, int32_t* expert_ids,
+                 int32_t* ntp, int32_t* inv_pos, const uint16_t* x, int xdtype, int64_t K, int64_t ldx, uint8_t* xq,
+                 int64_t ldq, float* xs) {
+    hipLaunchKernelGGL((moe_prep_kernel<PER, CPT>), grid, dim3(kPrepThreads), 0, stream, logits, ldtype, T, E, top_k,
+                       renorm, tw, ids, bm, P, sorted_ids, expert_ids, ntp, inv_pos, x, xdtype, K, ldx, xq, ldq, xs);
+  }
+  static void run(int cpt, const void* logits, int ldtype, int64_t T, int E, int top_k, int renorm, float* tw,
+                  int32_t* ids, int bm, int64_t P, int32_t* sorted_ids, int32_t* expert_ids, int32_t* ntp,
+                  int32_t* inv_pos, const void* x, int xdtype, int64_t K, int64_t ldx, uint8_t* xq, int64_t ldq,
+                  float* xs, hipStream_t stream) {
+    const dim3 grid((unsigned)(1 + (x ? T : 0)));
+    const uint16_t* xp = reinterpret_cast<const uint16_t*>(x);
+#define W4A8_PREP(C) go<C>(grid, stream, logits, ldtype, T, E, top_k, renorm, tw, ids, bm, P, sorted_ids, expert_ids, \
+                           ntp, inv_pos, xp, xdtype, K, ldx, xq, ldq, xs)
+    if (cpt == 1) W4A8_PREP(1);
+    else if (cpt == 2) W4A8_PREP(2);
+    else if (cpt == 4) W4A8_PREP(4);
+    else W4A8_PREP(0);
+#undef W4A8_PREP
+  }
+};
+
+bool moe_prep_fits(int64_t T, int top_k) { return T * top_k <= kPrepMaxSlots; }
+
+// Route + align (+ act quant of x when x is given) of a small batch in one launch; the caller
+// checks moe_prep_fits first.
+int launch_moe_prep(const void* logits, int ldtype, int64_t T, int E, int top_k, int renorm, float* tw,
+                    int32_t* ids, int bm, int64_t P, int32_t* sorted_ids, int32_t* expert_ids, int32_t* ntp,
+                    int32_t* inv_pos, const void* x, int xdtype, int64_t K, int64_t ldx, uint8_t* xq, int64_t ldq,
+                    float* xs, hipStream_t stream) {
+  if (T <= 0) return kOk;
+  const int c = quant_row_cpt(K, kPrepThreads);
+  const int cpt = c >= 1 && c <= 4 ? c : 0;
+  with_per<PrepLaunch>(E, cpt, logits, ldtype, T, E, top_k, renorm, tw, ids, bm, P, sorted_ids, expert_ids, ntp,
+                       inv_pos, x, xdtype, K, ldx, xq, ldq, xs, stream);
   return hipGetLastError() == hipSuccess ? kOk : kErrHip;
 }
 
 int launch_moe_combine(const float* y, int64_t ldy, const int32_t* inv_pos, const float* tw, int64_t T,
                        int top_k, int64_t H, void* out, int dtype, hipStream_t stream) {
   if (T <= 0) return kOk;
-  dim3 grid((unsigned)((H + 255) / 256), (unsigned)(T < 65535 ? T : 65535));
-  hipLaunchKernelGGL(moe_combine_kernel, grid, dim3(256), 0, stream, y, ldy, inv_pos, tw, T, top_k, H,
-                     out, dtype);
+  dim3 grid((unsigned)((H / 4 + 255) / 256), (unsigned)(T < 65535 ? T : 65535));
+  hipLaunchKernelGGL(moe_combine_kernel, grid, dim3(256), 0, stream, y, ldy, inv_pos, tw, T, top_k, H, out, dtype);
   return hipGetLastError() == hipSuccess ? kOk : kErrHip;
 }
 

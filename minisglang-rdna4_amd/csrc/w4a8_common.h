@@ -154,10 +154,44 @@ __device__ __forceinline__ uint8_t bload8(BufRsrc r, uint32_t voff, uint32_t sof
 
 // ---- per-token fp8 activation quant pieces (shared by the act-quant kernel and the decode GEMV's
 // fused prologue, so both produce the same codes bit for bit)
+//
+// Wave reductions: four DPP steps (lanes xor 1, xor 2, then the 8- and 16-lane mirrors) leave every
+// lane of each 16-lane row with the row's result, then four readlanes combine the rows. DPP moves
+// are plain VALU operands, so this costs tens of cycles where a shuffle (ds_bpermute) costs an
+// LDS round trip per step. All lanes must be active (uniform control flow).
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppRowMirror = 0x140, kDppHalfMirror = 0x141;
+template <int CTRL> __device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_mov_dpp(v, CTRL, 0xf, 0xf, false);
+}
+template <int CTRL> __device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(dpp_i<CTRL>(__float_as_int(v)));
+}
+__device__ __forceinline__ float lane_f(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// Workgroup barrier for LDS traffic only: waits for this wave's LDS operations, not for its global
+// stores in flight (which __syncthreads drains). For phases whose global stores no other wave of
+// the workgroup reads back. The memory clobber keeps the compiler from moving memory operations
+// across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// max is exact and order-free: every lane returns the same bits whatever the order
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  v = fmaxf(v, dpp_f<kDppXor1>(v));
+  v = fmaxf(v, dpp_f<kDppXor2>(v));
+  v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
+  v = fmaxf(v, dpp_f<kDppRowMirror>(v));
+  return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
+}
+
+// f32 sum in a fixed tree order; every lane returns the same bits
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp_f<kDppXor1>(v);
+  v += dpp_f<kDppXor2>(v);
+  v += dpp_f<kDppHalfMirror>(v);
+  v += dpp_f<kDppRowMirror>(v);
+  return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
 }
 
 // 8 bf16/fp16 values (one 16-byte load) -> f32

@@ -363,9 +363,48 @@ def _route_align(gating_output: torch.Tensor, top_k: int, renormalize: bool, num
                  block_size: int):
     """softmax + top-k + renormalize + align in one call (python/minisgl/quant/kernels.py:423-447).
     Returns (topk_weights f32, topk_ids i32, sorted_ids, expert_ids, num_tokens_post_pad)."""
-    tw, ids = _moe_route(gating_output, top_k, renormalize, num_experts)
-    sorted_ids, expert_ids, ntp, _ = _moe_align(ids, num_experts, block_size)
-    return tw, ids, sorted_ids, expert_ids, ntp
+    r = _route_align_quant(gating_output, top_k, renormalize, num_experts, block_size, None)
+    return r[0], r[1], r[2], r[3], r[4]
+
+
+def _route_align_quant(gating_output: torch.Tensor, top_k: int, renormalize: bool, num_experts: int,
+                       block_size: int, x: torch.Tensor | None):
+    """Route + align (+ per-token act quant of x when given) through w4a8_moe_route_align: one
+    launch for up to 256 slots. Returns (tw, ids, sorted_ids, expert_ids, ntp, inv_pos, x_fp8,
+    x_scales); the last two are None without x."""
+    engaged("w4a8_mi355x.moe_route_align")
+    g = gating_output.contiguous()
+    if g.dim() != 2 or g.shape[1] != num_experts:
+        raise AssertionError(f"moe route: gating_output must be (M, E={num_experts}), got {tuple(g.shape)}")
+    T = g.shape[0]
+    dev = g.device
+    numel = T * top_k
+    lib = _abi.load()
+    P = int(lib.w4a8_moe_padded_capacity(numel, num_experts, block_size))
+    tw = torch.empty((T, top_k), dtype=torch.float32, device=dev)
+    ids = torch.empty((T, top_k), dtype=torch.int32, device=dev)
+    sorted_ids = torch.empty((P,), dtype=torch.int32, device=dev)
+    expert_ids = torch.empty(((P + block_size - 1) // block_size,), dtype=torch.int32, device=dev)
+    ntp = torch.empty((1,), dtype=torch.int32, device=dev)
+    inv = torch.empty((max(numel, 1),), dtype=torch.int32, device=dev)
+    xq = xs = None
+    K = ldx = 0
+    xdt = 0
+    if x is not None:
+        xc = x if x.stride(-1) == 1 else x.contiguous()
+        K, ldx = xc.shape[1], xc.stride(0)
+        xdt = _abi.dtype_code(xc.dtype)
+        xq = torch.empty((T, K), dtype=torch.uint8, device=dev)
+        xs = torch.empty((T,), dtype=torch.float32, device=dev)
+        x = xc
+    _abi.check(lib.w4a8_moe_route_align(_abi.ptr(g), _abi.dtype_code(g.dtype), T, num_experts, top_k,
+                                        int(bool(renormalize)), block_size, P, _abi.ptr(tw), _abi.ptr(ids),
+                                        _abi.ptr(sorted_ids), _abi.ptr(expert_ids), _abi.ptr(ntp), _abi.ptr(inv),
+                                        _abi.ptr(x) if x is not None else None, xdt, K, ldx,
+                                        _abi.ptr(xq) if xq is not None else None, K,
+                                        _abi.ptr(xs) if xs is not None else None, _abi.stream_of(g)),
+               "moe_route_align")
+    return tw, ids, sorted_ids, expert_ids, ntp, inv, xq, xs
 
 
 def _moe_route(gating_output: torch.Tensor, top_k: int, renormalize: bool, num_experts: int):
@@ -516,27 +555,30 @@ def _moe_forward(x, w13, w13_scales, w13_zeros, w2, w2_scales, w2_zeros, gating_
     if block_m is None:
         block_m = _moe_block_m(M, E, top_k, flag_gemm1=True)
 
-    if topk_ids is None:
-        topk_weights, topk_ids = _moe_route(gating_output, top_k, renormalize, E)
-    else:
-        assert topk_weights is not None, "topk_weights required when topk_ids is given"
-        topk_weights = topk_weights.to(torch.float32).contiguous()
-        topk_ids = topk_ids.to(torch.int32).contiguous()
-        engaged("w4a8_mi355x.moe_align")
-    # the align's inverse positions (slot -> padded row) feed the combine
-    sorted_ids, expert_ids, ntp, inv = _moe_align(topk_ids, E, block_m)
-    P = sorted_ids.shape[0]
-    numel = topk_ids.numel()
-
     if x_fp8 is not None:
         assert act_scales is not None, "w4a8_moe: x_fp8 and act_scales must be supplied together"
         assert tuple(x_fp8.shape) == (M, K) and tuple(act_scales.shape) == (M,), (
             f"w4a8_moe: producer pair must be (M,K)=({M},{K}) and (M,)=({M},); got {tuple(x_fp8.shape)} and "
             f"{tuple(act_scales.shape)}")
-        xq, xs = _fp8_bytes(x_fp8).contiguous(), act_scales.to(torch.float32).contiguous()
     elif act_scales is not None:
         raise AssertionError("w4a8_moe: act_scales given without x_fp8")
+    xq = xs = None
+    if topk_ids is None:
+        # route + align, and the per-token quant of x unless the producer supplied it (one launch
+        # for small batches); the align's inverse positions (slot -> padded row) feed the combine
+        topk_weights, topk_ids, sorted_ids, expert_ids, ntp, inv, xq, xs = _route_align_quant(
+            gating_output, top_k, renormalize, E, block_m, x if x_fp8 is None else None)
     else:
+        assert topk_weights is not None, "topk_weights required when topk_ids is given"
+        topk_weights = topk_weights.to(torch.float32).contiguous()
+        topk_ids = topk_ids.to(torch.int32).contiguous()
+        engaged("w4a8_mi355x.moe_align")
+        sorted_ids, expert_ids, ntp, inv = _moe_align(topk_ids, E, block_m)
+    P = sorted_ids.shape[0]
+    numel = topk_ids.numel()
+    if x_fp8 is not None:
+        xq, xs = _fp8_bytes(x_fp8).contiguous(), act_scales.to(torch.float32).contiguous()
+    elif xq is None:
         xq, xs = act_quant(x)
 
     wfmt = _abi.W_E2M1 if weight_is_e2m1 else _abi.W_INT4

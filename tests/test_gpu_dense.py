@@ -43,7 +43,9 @@ def assert_close_to_oracle(got: torch.Tensor, ref: np.ndarray, what: str):
 
 # ------------------------------------------------------------------------------- act quant
 @pytest.mark.parametrize("dtype,code", [(torch.bfloat16, 0), (torch.float16, 1)])
-@pytest.mark.parametrize("M,K", [(1, 4096), (16, 2560), (7, 14336), (33, 768), (5, 28672)])
+# 64 rows or more of at most 4096 elements take the one-wave-per-row kernel
+@pytest.mark.parametrize("M,K", [(1, 4096), (16, 2560), (7, 14336), (33, 768), (5, 28672), (64, 768), (130, 4096),
+                                 (257, 2048), (70, 136)])
 def test_act_quant_bit_exact(kernels, oracle, dev, dtype, code, M, K):
     x = synth.activations(M, K, seed=M * 31 + K, outliers=True, dtype=dtype)
     x[0, :] = 0  # scale floor row

@@ -46,6 +46,47 @@ def test_route_align_bit_exact(kernels, oracle, dev, T):
     assert np.array_equal(inv.cpu().numpy()[: T * TOPK], rinv)
 
 
+@pytest.mark.parametrize("T", [1, 3, 16, 32, 33])
+def test_route_align_quant_bit_exact(kernels, oracle, dev, T):
+    """w4a8_moe_route_align with x: route and align equal the oracle's, and x's codes and scales
+    equal the act-quant kernel's, bit for bit. T*top_k <= 256 runs as one launch (one workgroup
+    routes and aligns, the others quantize rows); T = 33 (264 slots) takes the three-launch path."""
+    lg = synth.router_logits(T, E, seed=500 + T)
+    x = synth.activations(T, H, seed=T).to(dev)
+    x[0] = 0  # a zero row takes the 1e-8 scale floor
+    bm = 16
+    tw, ids, sorted_ids, expert_ids, ntp, inv, xq, xs = kernels._route_align_quant(lg.to(dev), TOPK, True, E, bm, x)
+    q, s = kernels.act_quant(x)
+    _sync()
+    assert torch.equal(xq, q) and torch.equal(xs, s)
+    rtw, rids = oracle.moe_route(lg.float().numpy(), TOPK, True)
+    assert np.array_equal(ids.cpu().numpy(), rids)
+    np.testing.assert_allclose(tw.cpu().numpy(), rtw, rtol=1e-6, atol=1e-7)
+    rs, re_, rntp, rinv = oracle.moe_align(rids, E, bm)
+    assert int(ntp.item()) == rntp
+    assert np.array_equal(sorted_ids.cpu().numpy(), rs)
+    assert np.array_equal(expert_ids.cpu().numpy(), re_)
+    assert np.array_equal(inv.cpu().numpy()[: T * TOPK], rinv)
+
+
+@pytest.mark.parametrize("E_,k,T", [(64, 6, 5), (256, 4, 8), (256, 4, 100), (512, 2, 7), (512, 16, 40), (20, 3, 9)])
+def test_route_align_expert_counts(kernels, oracle, dev, E_, k, T):
+    """Expert counts that put 1, 2, 4 or 8 experts on each lane, on both the one-launch path
+    (T*k <= 256) and the route + align kernels; fp32 logits with repeated values (ties)."""
+    g = torch.Generator().manual_seed(E_ + k + T)
+    lg = torch.randint(-4, 5, (T, E_), generator=g).float() * 0.25  # many exact ties
+    bm = 16
+    tw, ids, sorted_ids, expert_ids, ntp = kernels._route_align(lg.to(dev), k, True, E_, bm)
+    _sync()
+    rtw, rids = oracle.moe_route(lg.numpy(), k, True)
+    assert np.array_equal(ids.cpu().numpy(), rids)
+    np.testing.assert_allclose(tw.cpu().numpy(), rtw, rtol=1e-6, atol=1e-7)
+    rs, re_, rntp, _ = oracle.moe_align(rids, E_, bm)
+    assert int(ntp.item()) == rntp
+    assert np.array_equal(sorted_ids.cpu().numpy(), rs)
+    assert np.array_equal(expert_ids.cpu().numpy(), re_)
+
+
 def test_route_ties_keep_lower_index(kernels, dev):
     lg = torch.zeros(3, 16)
     lg[0] = torch.tensor([0.5, 1, 1, 1, -1, 1, 0, 2, 0, 0, 0, 0, 0, 0, 0, 0])
