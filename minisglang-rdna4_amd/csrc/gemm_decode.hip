@@ -28,8 +28,17 @@ GemvPlan plan_gemv(const GemmArgs& p, int64_t row_blocks, bool quant_src) {
   if (w < 1) w = 1;
   const int64_t groups = (strips + pl.nstr - 1) / pl.nstr * row_blocks;
   while (w > 1 && groups * w > 8192 && (KT + w - 1) / w < 8) w = (w + 1) / 2;
-  const int64_t tpw = (KT + w - 1) / w;
+  int64_t tpw = (KT + w - 1) / w;
   w = (KT + tpw - 1) / tpw;
+  // grids of under ~2 waves per SIMD (the MoE decode calls, a handful of experts): halve the tiles
+  // per wave, down to 2 and up to 8 waves, so more of the weight bytes are in flight at once
+  while (groups * w < 2048 && w < 8) {
+    const int64_t t2 = (tpw + 1) / 2;
+    const int64_t w2 = (KT + t2 - 1) / t2;
+    if (t2 < 2 || w2 > 8) break;
+    tpw = t2;
+    w = w2;
+  }
   pl.waves = (int)w;
   pl.tpw = (int)tpw;
 
