@@ -17,11 +17,11 @@ __device__ __forceinline__ float block_max(float v, float* red) {
   const int tid = threadIdx.x;
   v = wave_max(v);
   if ((tid & 63) == 0) red[tid >> 6] = v;
-  __syncthreads();
+  lds_barrier();
   v = red[0];
 #pragma unroll
   for (int w = 1; w < NT / 64; ++w) v = fmaxf(v, red[w]);
-  __syncthreads();
+  lds_barrier();
   return v;
 }
 

@@ -34,22 +34,6 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (0 << 8) | ((N >> 4) << 14));
 }
 
-// LDS-DMA of `bytes` (1 or 16) per lane into lds + lane * bytes. The generic-to-LDS pointer cast
-// only exists for the device target, so the host pass (which only needs the kernel's launch
-// stub) compiles an empty body.
-__device__ __forceinline__ void lds_dma16(BufRsrc r, unsigned char* lds, uint32_t voff, uint32_t soff) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
-#endif
-}
-// (an LDS-DMA lane always lands 4 bytes at lds + lane * 4, whatever the load size: E8M0 bytes
-// travel as dwords)
-__device__ __forceinline__ void lds_dma4(BufRsrc r, unsigned char* lds, uint32_t voff, uint32_t soff) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 4, voff, soff, 0, 0);
-#endif
-}
-
 template <int WM, int WN, int RB, int NSB, int MODE>
 __global__ void __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 gemm_dma_kernel(const GemmArgs p) {

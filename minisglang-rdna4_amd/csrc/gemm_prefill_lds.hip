@@ -290,7 +290,7 @@ gemm_lds_kernel(const GemmArgs p) {
   issue(0, Set0{});
   commit(0, Set0{});
   if (KT > 1) issue(1, Set1{});
-  __syncthreads();
+  lds_barrier();
   int kt = 0;
   for (; kt + 3 < KT; kt += 2) {
     issue(kt + 2, Set0{});
@@ -298,13 +298,13 @@ gemm_lds_kernel(const GemmArgs p) {
     compute(0);
     __builtin_amdgcn_sched_barrier(0);
     commit(1, Set1{});
-    __syncthreads();
+    lds_barrier();
     issue(kt + 3, Set1{});
     __builtin_amdgcn_sched_barrier(0);
     compute(1);
     __builtin_amdgcn_sched_barrier(0);
     commit(0, Set0{});
-    __syncthreads();
+    lds_barrier();
   }
   // drain: 1, 2 or 3 steps left (step kt is in stage 0, step kt + 1 in registers set 1)
   const int left = KT - kt;
@@ -314,17 +314,17 @@ gemm_lds_kernel(const GemmArgs p) {
     compute(0);
     __builtin_amdgcn_sched_barrier(0);
     commit(1, Set1{});
-    __syncthreads();
+    lds_barrier();
     compute(1);
     __builtin_amdgcn_sched_barrier(0);
     commit(0, Set0{});
-    __syncthreads();
+    lds_barrier();
     compute(0);
   } else if (left == 2) {
     compute(0);
     __builtin_amdgcn_sched_barrier(0);
     commit(1, Set1{});
-    __syncthreads();
+    lds_barrier();
     compute(1);
   } else {
     compute(0);

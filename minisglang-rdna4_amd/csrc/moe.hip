@@ -283,7 +283,7 @@ moe_prep_kernel(const void* __restrict__ logits, int ldtype, int64_t T, int E, i
   __shared__ int32_t ids_s[kPrepMaxSlots];
   for (int64_t t = threadIdx.x >> 6; t < T; t += kPrepThreads / 64)
     route_token<PER>(logits, ldtype, t, E, top_k, renorm, tw, ids, ids_s);
-  __syncthreads();
+  lds_barrier();
   align_block<kPrepThreads, 64 * PER, 0>(ids_s, T * top_k, E, bm, P, sorted_ids, expert_ids, ntp, inv_pos);
 }
 

@@ -152,6 +152,23 @@ __device__ __forceinline__ uint8_t bload8(BufRsrc r, uint32_t voff, uint32_t sof
   return __builtin_amdgcn_raw_buffer_load_b8(r, voff, soff, 0);
 }
 
+// LDS-DMA (buffer_load ... lds) of 16 (or 4) bytes per lane into lds + lane * 16 (lane * 4): the
+// buffer unit writes LDS directly, no VGPR holds the data, and the wave's vmcnt tracks completion.
+// The generic-to-LDS pointer cast only exists for the device target, so the host pass (which only
+// needs the kernels' launch stubs) compiles an empty body.
+__device__ __forceinline__ void lds_dma16(BufRsrc r, unsigned char* lds, uint32_t voff, uint32_t soff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
+#endif
+}
+// (an LDS-DMA lane always lands 4 bytes at lds + lane * 4, whatever the load size: E8M0 bytes
+// travel as dwords)
+__device__ __forceinline__ void lds_dma4(BufRsrc r, unsigned char* lds, uint32_t voff, uint32_t soff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 4, voff, soff, 0, 0);
+#endif
+}
+
 // ---- per-token fp8 activation quant pieces (shared by the act-quant kernel and the decode GEMV's
 // fused prologue, so both produce the same codes bit for bit)
 //
@@ -171,9 +188,10 @@ __device__ __forceinline__ float lane_f(float v, int l) {
 }
 
 // Workgroup barrier for LDS traffic only: waits for this wave's LDS operations, not for its global
-// stores in flight (which __syncthreads drains). For phases whose global stores no other wave of
-// the workgroup reads back. The memory clobber keeps the compiler from moving memory operations
-// across it.
+// loads and stores in flight (__syncthreads waits for every outstanding memory operation of the
+// wave, which would drain a window of weight loads issued ahead of it). Register results of global
+// loads are still waited for where they are used, as always. For data shared through LDS only; the
+// memory clobber keeps the compiler from moving memory operations across it.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // max is exact and order-free: every lane returns the same bits whatever the order
