@@ -220,8 +220,9 @@ gemm_dma_kernel(const GemmArgs p) {
   const int zsh = 4 * (lane & 7);
 
   // MFMA work of one K step from stage I (operands read one row block / strip ahead of their
-  // MFMAs)
-  auto compute = [&](auto I) __attribute__((always_inline)) {
+  // MFMAs). int4: mid() runs right after the first strip's MFMAs are issued, so its VALU work
+  // (the unpack of the next step's weights) overlaps MFMAs in flight.
+  auto compute = [&](auto I, auto mid) __attribute__((always_inline)) {
     const unsigned char* st = stage(I);
     if constexpr (kFp4) {
       uint4 braw[NSB];
@@ -270,6 +271,7 @@ gemm_dma_kernel(const GemmArgs p) {
           __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
           for (int rb = 0; rb < RB; ++rb) cj[rb] = mfma_f8f8(a[rb], b, MODE == kPSym ? pre[rb] : zero4);
+          if (j == 0) mid();
         }
         if (j > 0) {
 #pragma unroll
@@ -298,9 +300,8 @@ gemm_dma_kernel(const GemmArgs p) {
     constexpr int c = decltype(C)::value, n1 = (c + 1) % 3, n2 = (c + 2) % 3;
     issue(IC<n2>{}, kt + 2);
     __builtin_amdgcn_sched_barrier(0);
-    compute(C);
+    compute(C, [&]() __attribute__((always_inline)) { commit(IC<n1>{}, IC<n1>{}); });
     __builtin_amdgcn_sched_barrier(0);
-    commit(IC<n1>{}, IC<n1>{});
     wait_vm_lgkm0<NOPS>();
     __builtin_amdgcn_s_barrier();
   };
@@ -310,8 +311,9 @@ gemm_dma_kernel(const GemmArgs p) {
     if (kt >= KT) return;
     const bool more = kt + 2 < KT;
     if (more) issue(IC<n2>{}, kt + 2);
-    compute(C);
-    if (kt + 1 < KT) commit(IC<n1>{}, IC<n1>{});
+    compute(C, [&]() __attribute__((always_inline)) {
+      if (kt + 1 < KT) commit(IC<n1>{}, IC<n1>{});
+    });
     if (more) wait_vm_lgkm0<NOPS>();
     else wait_vm_lgkm0<0>();
     __builtin_amdgcn_s_barrier();
