@@ -18,6 +18,10 @@ zero-point int4, M=16, K=2560, N=9728), cfg4 (MoE E=128 top-8 H=2048 I=768, T in
 and cfg5 (MXFP4 E8M0, K x N in {8192x28672, 28672x8192}, M in {1,16,4096}); GB/s against 8 TB/s
 for the decode sizes, TFLOPS against the 5 PFLOPS fp8 peak for the large ones.
 
+producer_norm_step times the same sweep with its inputs coming out of the RMSNorm + residual-add
+producer: once with the linear quantizing its bf16 input, once with the producer's fp8 pair
+(no act-quant launches).
+
 Modes for profiling runs (same committed file): --profile-kernel runs only the roofline loop,
 --copy-calib runs a plain device copy of known size (for scaling rocprofv3 byte counters).
 """
@@ -252,6 +256,59 @@ def configs_leg(kernels, dev) -> dict:
     return out
 
 
+def producer_leg(kernels, dev, weights, steps: int = 100) -> dict:
+    """The configs[1] sweep with its activations produced by the RMSNorm + residual-add producer, in
+    two graph-replayed steps of 20 (norm, linear) pairs: `in_op_quant` runs rms_norm_add then
+    w4a8_linear on bf16 x (the linear quantizes), `producer_pair` runs rms_norm_add_quant then
+    w4a8_linear on the (x_fp8, act_scales) pair it emitted. Same weights as the headline step."""
+    import torch
+
+    norm = importlib.import_module("minisglang-rdna4_amd.layers.norm")
+    gen = torch.Generator(device=dev).manual_seed(77)
+    xs = [[make_x(M, K, 3000 + 10 * i + j, dev) for j, (K, N) in enumerate(SHAPES)] for i, M in enumerate(MS)]
+    rs = [[make_x(M, K, 4000 + 10 * i + j, dev) for j, (K, N) in enumerate(SHAPES)] for i, M in enumerate(MS)]
+    gains = {K: (torch.randn(K, generator=gen, device=dev) * 0.1 + 1.0).to(torch.bfloat16) for K, _ in SHAPES}
+
+    def step(pair: bool):
+        outs = []
+        for i, M in enumerate(MS):
+            for j, (K, N) in enumerate(SHAPES):
+                t, sc = weights[i][j]
+                if pair:
+                    h, q, s = norm._rms_norm_add_quant(xs[i][j], rs[i][j], gains[K], 1e-6)
+                    outs.append(kernels.w4a8_linear(h, t, sc, None, GROUP, x_fp8=q, act_scales=s))
+                else:
+                    h = norm._rms_norm_add(xs[i][j], rs[i][j], gains[K], 1e-6)
+                    outs.append(kernels.w4a8_linear(h, t, sc, None, GROUP))
+        return outs
+
+    out = {}
+    for name, pair in (("in_op_quant", False), ("producer_pair", True)):
+        step(pair)
+        torch.cuda.synchronize()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            step(pair)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            keep = step(pair)
+        for _ in range(10):
+            graph.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            graph.replay()
+        torch.cuda.synchronize()
+        out[name] = {"us_per_step": round((time.perf_counter() - t0) * 1e6 / steps, 1)}
+        del graph, keep
+    out["launches_per_step"] = {"in_op_quant": "20 norms + 14 act-quant + 20 GEMV",
+                                "producer_pair": "20 norms (with the quant epilogue) + 20 GEMV"}
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -335,6 +392,7 @@ def main() -> int:
     roof = roofline_leg(kernels, dev)
     prefill = None if args.no_prefill else prefill_leg(kernels, dev)
     others = None if args.no_configs else configs_leg(kernels, dev)
+    producer = None if args.no_configs else producer_leg(kernels, dev, weights)
     cpu = None if args.no_cpu_baseline else cpu_baseline_leg()
 
     line = {
@@ -365,6 +423,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "prefill_config3": prefill,
         "other_configs": others,
+        "producer_norm_step": producer,
     }
     print(json.dumps(line))
     return 0

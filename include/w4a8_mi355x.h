@@ -104,6 +104,17 @@ int w4a8_moe_route_align(const void* logits, int logits_dtype, int64_t T, int64_
                          int32_t* expert_ids, int32_t* ntp, int32_t* inv_pos, const void* x, int x_dtype, int64_t K,
                          int64_t ldx, uint8_t* x_fp8, int64_t ldq, float* x_scales, void* stream);
 
+/* RMSNorm producer with the per-token fp8 quant of its output as an epilogue. Replaces tail_hip's
+ * rms_norm / rms_norm_add / rms_norm_quant / rms_norm_add_quant (python/minisgl/layers/norm.py:9-58,
+ * 134-168): with residual non-NULL, residual <- x + residual (in place, in the activation dtype) and
+ * the norm runs over that sum; out = dtype(dtype(v * rsqrt(mean(v^2) + eps)) * g), g = weight,
+ * dtype(weight + 1) with plus_one, none with weight NULL. With x_fp8/act_scales non-NULL it also
+ * writes the pair w4a8_act_quant(out) would give, bit for bit, for a w4a8 linear to consume. out may
+ * be x; K <= 32768. */
+int w4a8_rms_norm(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, void* residual, int64_t ldr,
+                  const void* weight, int plus_one, float eps, void* out, int64_t ldo, uint8_t* x_fp8, int64_t ldq,
+                  float* act_scales, void* stream);
+
 /* Padded capacity numel + (E+1)*(block_m-1) of sorted_ids (python/minisgl/moe/fused.py:94). */
 int64_t w4a8_moe_padded_capacity(int64_t numel, int64_t E, int block_m);
 

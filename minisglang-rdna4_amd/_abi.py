@@ -36,6 +36,8 @@ SIGNATURES = {
     "w4a8_linear": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _c_i64, _vp, _c_i64, _vp, _c_int, _vp, _c_int, _c_i64,
                              _vp, _c_int, _c_i64, _c_int, _vp, _c_i64, _c_int, _vp]),
     "w4a8_moe_route": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _c_int, _c_int, _vp, _vp, _vp]),
+    "w4a8_rms_norm": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _c_i64, _vp, _c_i64, _vp, _c_int, ctypes.c_float, _vp,
+                               _c_i64, _vp, _c_i64, _vp, _vp]),
     "w4a8_moe_route_align": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_i64, _vp, _vp, _vp,
                                       _vp, _vp, _vp, _vp, _c_int, _c_i64, _c_i64, _vp, _c_i64, _vp, _vp]),
     "w4a8_moe_padded_capacity": (_c_i64, [_c_i64, _c_i64, _c_int]),

@@ -24,6 +24,9 @@ int launch_moe_align(const int32_t* ids, int64_t numel, int E, int bm, int64_t P
 int launch_moe_combine(const float* y, int64_t ldy, const int32_t* inv_pos, const float* tw, int64_t T,
                        int top_k, int64_t H, void* out, int dtype, hipStream_t stream);
 bool moe_prep_fits(int64_t T, int top_k);
+int launch_rms_norm(const void* x, int64_t ldx, void* res, int64_t ldr, const void* weight, int plus_one, float eps,
+                    int64_t M, int64_t K, int dtype, void* out, int64_t ldo, uint8_t* q, int64_t ldq, float* scales,
+                    hipStream_t stream);
 int launch_moe_prep(const void* logits, int ldtype, int64_t T, int E, int top_k, int renorm, float* tw,
                     int32_t* ids, int bm, int64_t P, int32_t* sorted_ids, int32_t* expert_ids, int32_t* ntp,
                     int32_t* inv_pos, const void* x, int xdtype, int64_t K, int64_t ldx, uint8_t* xq, int64_t ldq,
@@ -95,6 +98,25 @@ int w4a8_act_quant(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx
   if (!aligned16(x) || !aligned16(x_fp8)) return fail(kErrInvalid, "act_quant: x and x_fp8 must be 16-byte aligned");
   return hip_status(launch_act_quant(x, x_dtype, M, K, ldx, x_fp8, ldq, act_scales, row_count, (hipStream_t)stream),
                     "act_quant");
+}
+
+int w4a8_rms_norm(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, void* residual, int64_t ldr,
+                  const void* weight, int plus_one, float eps, void* out, int64_t ldo, uint8_t* x_fp8, int64_t ldq,
+                  float* act_scales, void* stream) {
+  if (x_dtype != kBF16 && x_dtype != kF16) return fail(kErrInvalid, "rms_norm: x must be bf16 or fp16");
+  if (M < 0 || K <= 0 || K % 8) return fail(kErrInvalid, "rms_norm: K=%lld must be a positive multiple of 8", (long long)K);
+  if (K > 32768) return fail(kErrUnsupported, "rms_norm: rows of K=%lld > 32768 elements", (long long)K);
+  if (ldx < K || ldx % 8 || ldo < K || ldo % 8 || (residual && (ldr < K || ldr % 8)) || (x_fp8 && (ldq < K || ldq % 8)))
+    return fail(kErrInvalid, "rms_norm: row strides must be >= K and multiples of 8");
+  if (!aligned16(x) || !aligned16(out) || (residual && !aligned16(residual)) || (weight && !aligned16(weight)) ||
+      (x_fp8 && !aligned16(x_fp8)))
+    return fail(kErrInvalid, "rms_norm: x, out, residual, weight and x_fp8 must be 16-byte aligned");
+  if (!x_fp8 != !act_scales) return fail(kErrInvalid, "rms_norm: x_fp8 and act_scales must be supplied TOGETHER");
+  if (residual && (residual == x || residual == out))
+    return fail(kErrInvalid, "rms_norm: residual must not share storage with x or out");
+  if (!(eps >= 0.0f)) return fail(kErrInvalid, "rms_norm: eps must be >= 0");
+  return hip_status(launch_rms_norm(x, ldx, residual, ldr, weight, plus_one, eps, M, K, x_dtype, out, ldo, x_fp8, ldq,
+                                    act_scales, (hipStream_t)stream), "rms_norm");
 }
 
 int64_t w4a8_tile_bytes(int64_t N, int64_t K) {

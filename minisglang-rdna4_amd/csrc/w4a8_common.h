@@ -99,13 +99,21 @@ __device__ __forceinline__ v8i splat8(uint32_t v) {
 // bf16 / fp16 scalar helpers (RNE)
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+  // round to nearest even; NaN keeps its top bits and is made quiet. Written as a select so that a
+  // conversion costs no branch.
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t rne = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  const uint32_t nan = (u >> 16) | 0x40u;
+  return (uint16_t)(((u & 0x7fffffffu) > 0x7f800000u) ? nan : rne);
 }
 __device__ __forceinline__ float f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
-__device__ __forceinline__ uint16_t f32_to_f16(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+// The empty asm pins f as an f32 value: without it the compiler may contract a producing f32
+// multiply and this conversion into one mixed-precision op (v_mad_mixlo_f16) with a single
+// rounding, where the f32 product and then the f16 conversion round twice.
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+  asm volatile("" : "+v"(f));
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
 
 __device__ __forceinline__ float load_act(const uint16_t* p, int dtype) {
   return dtype == kBF16 ? bf16_to_f32(*p) : f16_to_f32(*p);

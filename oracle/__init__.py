@@ -56,6 +56,8 @@ def lib() -> ctypes.CDLL:
         L.w4o_moe_forward.restype = None
         L.w4o_moe_forward.argtypes = [vp, ci, i64, i64, i64, i64, i64, vp, vp, vp, ctypes.c_int32, i64,
                                       vp, vp, vp, vp, vp, vp, ci, ci, i64, i64, vp, vp]
+        L.w4o_rms_norm.restype = None
+        L.w4o_rms_norm.argtypes = [vp, vp, vp, ci, f, ci, i64, i64, vp]
         L.w4o_silu_mul.restype = ctypes.c_uint16
         L.w4o_silu_mul.argtypes = [ctypes.c_double, ctypes.c_double, ci]
         L.w4o_bf16_to_f32.restype = f
@@ -194,3 +196,15 @@ def moe_forward(x_bits, dtype, tw, sorted_ids, expert_ids, ntp, bm, top_k, w13, 
 
 def silu_mul(gate: float, up: float, dtype: int = 0) -> int:
     return int(lib().w4o_silu_mul(gate, up, dtype))
+
+
+def rms_norm(x_bits: np.ndarray, weight_bits: np.ndarray | None, eps: float, dtype: int = 0, plus_one: bool = False,
+             residual_bits: np.ndarray | None = None):
+    """RMSNorm (+ residual add) over (M, K) bf16/fp16 bit patterns -> (out bits, new residual bits or None)."""
+    x = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    M, K = x.shape
+    out = np.empty_like(x)
+    res = None if residual_bits is None else np.ascontiguousarray(residual_bits, dtype=np.uint16).copy()
+    w = None if weight_bits is None else np.ascontiguousarray(weight_bits, dtype=np.uint16)
+    lib().w4o_rms_norm(_p(x), _p(res), _p(w), int(plus_one), float(eps), dtype, M, K, _p(out))
+    return out, res

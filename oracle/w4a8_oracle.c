@@ -374,3 +374,80 @@ void w4o_moe_forward(const uint16_t* x, int dtype, int64_t T, int64_t H, int64_t
   }
   free(y2); free(b2q); free(b2); free(h); free(xs); free(xq);
 }
+
+/* ------------------------------------------------------------------------------------------ */
+/* RMSNorm (+ residual add) producer: restates python/minisgl/layers/norm.py:9-24 (the torch   */
+/* decomposition: f32-widened mean of squares, rsqrt(var + eps), rounded to dtype, times the   */
+/* gain in dtype; plus_one uses dtype(weight + 1); no weight = unweighted) and :134-138 / :145- */
+/* 168 (rms_norm_add: residual <- x + residual in dtype, normed over the sum). The fp8 pair of  */
+/* rms_norm_quant is w4o_act_quant over the rounded output (norm.py:27-46,                      */
+/* tools/w4a8_producer_actquant.py:113-136).                                                    */
+/* The f32 sum of squares follows a fixed order (the order is this build's; the external       */
+/* kernel's is unpinned): NT partial sums (NT = 256 for K <= 2048, 512 for K <= 4096, else      */
+/* 1024), partial t accumulating elements (c*NT + t)*8 + i for c = 0, 1, ... and i = 0..7 with  */
+/* fmaf; each 64-partial wave summed pairwise by lane xor 1, xor 2, then the 8- and 16-lane     */
+/* mirrors, then (row 0 + row 1) + (row 2 + row 3); the NT/64 wave sums in a balanced pairwise  */
+/* tree. mean = sum / K; rstd = 1 / sqrt(mean + eps).                                            */
+/* residual (in/out) and weight may be NULL. out may be x.                                      */
+/* ------------------------------------------------------------------------------------------ */
+static float wave_sum64(const float* in) {
+  float v[64], t[64];
+  memcpy(v, in, sizeof v);
+  for (int l = 0; l < 64; ++l) t[l] = v[l] + v[l ^ 1];
+  memcpy(v, t, sizeof v);
+  for (int l = 0; l < 64; ++l) t[l] = v[l] + v[l ^ 2];
+  memcpy(v, t, sizeof v);
+  for (int l = 0; l < 64; ++l) t[l] = v[l] + v[(l & ~7) | (7 - (l & 7))];
+  memcpy(v, t, sizeof v);
+  for (int l = 0; l < 64; ++l) t[l] = v[l] + v[(l & ~15) | (15 - (l & 15))];
+  memcpy(v, t, sizeof v);
+  return (v[0] + v[16]) + (v[32] + v[48]);
+}
+
+void w4o_rms_norm(const uint16_t* x, uint16_t* residual, const uint16_t* weight, int plus_one, float eps,
+                  int dtype, int64_t M, int64_t K, uint16_t* out) {
+  float* row = (float*)malloc(sizeof(float) * (size_t)K);
+  for (int64_t m = 0; m < M; ++m) {
+    for (int64_t k = 0; k < K; ++k) {
+      float v = from_dt(x[m * K + k], dtype);
+      if (residual) {
+        uint16_t s = to_dt(v + from_dt(residual[m * K + k], dtype), dtype);
+        residual[m * K + k] = s;
+        v = from_dt(s, dtype);
+      }
+      row[k] = v;
+    }
+    const int NT = K <= 2048 ? 256 : K <= 4096 ? 512 : 1024, NW = NT / 64;
+    float part[1024];
+    for (int t = 0; t < NT; ++t) {
+      float ss = 0.0f;
+      for (int64_t c = 0; c * NT * 8 < K; ++c)
+        for (int i = 0; i < 8; ++i) {
+          int64_t k = (c * NT + t) * 8 + i;
+          float f = k < K ? row[k] : 0.0f;
+          ss = fmaf(f, f, ss);
+        }
+      part[t] = ss;
+    }
+    float w[16];
+    for (int q = 0; q < NW; ++q) w[q] = wave_sum64(part + 64 * q);
+    for (int st = 1; st < NW; st <<= 1)
+      for (int q = 0; q + st < NW; q += 2 * st) w[q] = w[q] + w[q + st];
+    volatile float sum = w[0];
+    volatile float mean = sum / (float)K;
+    volatile float den = sqrtf(mean + eps);
+    volatile float rstd = 1.0f / den;
+    for (int64_t k = 0; k < K; ++k) {
+      volatile float nv = row[k] * rstd;
+      float o = from_dt(to_dt(nv, dtype), dtype);
+      if (weight) {
+        float g = from_dt(weight[k], dtype);
+        if (plus_one) g = from_dt(to_dt(g + 1.0f, dtype), dtype);
+        volatile float prod = o * g;
+        o = from_dt(to_dt(prod, dtype), dtype);
+      }
+      out[m * K + k] = to_dt(o, dtype);
+    }
+  }
+  free(row);
+}

@@ -51,11 +51,11 @@ def _ctype_of(decl: str):
     decl = decl.replace("const ", "").strip()
     if "*" in decl:
         return ctypes.c_void_p if decl not in ("char*", "char *") else ctypes.c_char_p
-    return {"int": ctypes.c_int, "int64_t": ctypes.c_int64}[decl]
+    return {"int": ctypes.c_int, "int64_t": ctypes.c_int64, "float": ctypes.c_float}[decl]
 
 
 def test_bindings_match_header_prototypes():
-    """Each ctypes signature has the header's parameter count and kinds (pointer / int / int64)."""
+    """Each ctypes signature has the header's parameter count and kinds (pointer / int / int64 / float)."""
     abi = pkg("_abi")
     protos = _declared_params()
     assert sorted(protos) == _declared()

@@ -294,3 +294,54 @@ def test_moe_forward_matches_composition(oracle):
             y = oracle.gemm(q2, s2v, w2[e], s2[e], None, g)[0]
             ref[t] += tw[t, j] * y
     np.testing.assert_allclose(out, ref, rtol=1e-9, atol=1e-9)
+
+
+# ------------------------------------------------------------------------------- RMSNorm producer
+def _bits(t):
+    return synth.bits16(t)
+
+
+def _from_bits(b, dtype):
+    return torch.from_numpy(np.ascontiguousarray(b).view(np.int16)).view(dtype)
+
+
+@pytest.mark.parametrize("dtype,code", [(torch.bfloat16, 0), (torch.float16, 1)])
+@pytest.mark.parametrize("K", [2048, 2816, 5120, 13, 8])
+def test_rms_norm_matches_torch_decomposition(oracle, dtype, code, K):
+    """The oracle's norm against the reference's own torch decomposition (python/minisgl/layers/
+    norm.py:19-24: f32 mean of squares, rsqrt, round to dtype, times the gain in dtype), including
+    plus_one and the unweighted form. The two sum the squares in different orders, so a last-bit
+    difference in the mean may move a rounding: at most 1 output ulp, on a small share of elements."""
+    if K % 8:
+        K = 8 * K  # rows are whole 16-byte chunks on the device; the oracle itself takes any K
+    g = torch.Generator().manual_seed(K + code)
+    M = 6
+    x = (torch.randn(M, K, generator=g) * 0.7).to(dtype)
+    x[0] = 0  # an all-zero row: rstd = 1/sqrt(eps), output zero
+    w = (torch.randn(K, generator=g) * 0.1 + 1.0).to(dtype)
+    for weight, plus_one in ((w, False), (w - 1.0, True), (None, False)):
+        o, _ = oracle.rms_norm(_bits(x), None if weight is None else _bits(weight.to(dtype)), 1e-6, code, plus_one)
+        xf = x.float()
+        var = xf.pow(2).mean(dim=-1, keepdim=True)
+        ref = (xf * torch.rsqrt(var + 1e-6)).to(dtype)
+        if weight is not None:
+            ref = ref * (weight.to(dtype) + 1.0) if plus_one else ref * weight.to(dtype)
+        got = _from_bits(o, dtype)
+        diff = (got.view(torch.int16).int() - ref.view(torch.int16).int()).abs()
+        assert int(diff.max()) <= 1, f"K={K} plus_one={plus_one}: {int(diff.max())} ulp"
+        assert float((diff > 0).float().mean()) < 0.01
+        assert torch.equal(got[0], torch.zeros(K, dtype=dtype))
+
+
+def test_rms_norm_add_residual_is_dtype_sum(oracle):
+    """rms_norm_add: residual <- x + residual with one rounding to the dtype (torch's bf16 add), and
+    the norm runs over that sum (python/minisgl/layers/norm.py:134-138)."""
+    g = torch.Generator().manual_seed(5)
+    for dtype, code in ((torch.bfloat16, 0), (torch.float16, 1)):
+        x = torch.randn(4, 2048, generator=g).to(dtype)
+        r = torch.randn(4, 2048, generator=g).to(dtype)
+        w = (torch.randn(2048, generator=g) * 0.1 + 1).to(dtype)
+        o, nr = oracle.rms_norm(_bits(x), _bits(w), 1e-5, code, False, residual_bits=_bits(r))
+        assert torch.equal(_from_bits(nr, dtype), x + r)
+        o2, _ = oracle.rms_norm(_bits(x + r), _bits(w), 1e-5, code, False)
+        assert np.array_equal(o, o2)
