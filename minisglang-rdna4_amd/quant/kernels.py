@@ -600,7 +600,10 @@ def _moe_forward(x, w13, w13_scales, w13_zeros, w2, w2_scales, w2_zeros, gating_
     q2 = torch.empty((P, inter), dtype=torch.uint8, device=x.device)
     s2 = torch.empty((P,), dtype=torch.float32, device=x.device)
     lib = _abi.load()
-    _abi.check(lib.w4a8_act_quant(_abi.ptr(buf2), _abi.dtype_code(x.dtype), P, inter, inter, _abi.ptr(q2), inter,
+    # rows that can hold data: every expert with slots pads to whole blocks, so ntp <= this bound;
+    # the kernel reads ntp on the device and skips the rest, the bound only sizes the grid
+    rows = min(P, (numel // block_m + min(E, numel)) * block_m)
+    _abi.check(lib.w4a8_act_quant(_abi.ptr(buf2), _abi.dtype_code(x.dtype), rows, inter, inter, _abi.ptr(q2), inter,
                                   _abi.ptr(s2), _abi.ptr(ntp), _abi.stream_of(x)), "w4a8_moe act_quant(gemm2)")
     y2 = torch.empty((P, K), dtype=torch.float32, device=x.device)
     engaged(f"w4a8_mi355x.moe_gemm2({arm_name}{e2})")
