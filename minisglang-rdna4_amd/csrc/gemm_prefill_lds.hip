@@ -332,34 +332,7 @@ gemm_lds_kernel(const GemmArgs p) {
 
   // epilogue: lane holds rows 4*(lane>>4)+r of each row block, channel (lane & 15) of each strip
   const int64_t row0 = blk_row0 + (int64_t)wm * RB * 16;
-  const int jn = p.silu ? NSB / 2 : NSB;
-#pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int64_t row = row0 + rb * 16 + 4 * (lane >> 4) + r;
-      int64_t ar;
-      if (!lrow_source(p, row, ar)) continue;
-      const float s = p.act_scales[ar];
-#pragma unroll
-      for (int j = 0; j < NSB; ++j) {
-        if (j >= jn) continue;
-        bool ok;
-        const int gs = gstrip(sl[j], ok);
-        if (!ok) continue;
-        const int64_t col = (int64_t)gs * kTileN + (lane & 15);
-        float v;
-        if (p.silu)
-          v = lsilu_mul(acc[rb][j][r] * s, acc[rb][j + NSB / 2][r] * s, p.out_dtype);
-        else
-          v = acc[rb][j][r] * s;
-        if (p.out_dtype == kF32)
-          reinterpret_cast<float*>(p.out)[row * p.ldo + col] = v;
-        else
-          reinterpret_cast<uint16_t*>(p.out)[row * p.ldo + col] = to_dtype(v, p.out_dtype);
-      }
-    }
-  }
+  store_tile(p, acc, row0, lane, [&](int j, bool& ok) __attribute__((always_inline)) { return gstrip(sl[j], ok); });
 }
 
 template <int WM, int WN, int RB, int NSB, int MODE, int WPE>

@@ -46,6 +46,69 @@ struct LdsStage {
   static constexpr int kBytes = kA + kB + kS + kZ;
 };
 
+// Epilogue of the LDS-staged GEMMs. Lane layout: rows row0 + rb*16 + 4*(lane>>4) + r, channel
+// (lane & 15) of each strip j, strip(j, ok) giving strip j's global index. y = acc * s_row, or for
+// the fused arm silu(gate) * up over the strip pairs (j, j + NSB/2), rounded to the output dtype.
+// The dtype and the arm are compile-time here, so the store loops hold no branches and no loads.
+template <int DT, bool SILU, int RB, int NSB, typename SF>
+__device__ __forceinline__ void store_tile_dt(const GemmArgs& p, const v4f (&acc)[RB][NSB], const float (&sc)[RB][4],
+                                              uint32_t valid, int64_t row0, int lane, SF strip) {
+  constexpr int JN = SILU ? NSB / 2 : NSB;
+#pragma unroll
+  for (int j = 0; j < JN; ++j) {
+    bool ok;
+    const int gs = strip(j, ok);
+    if (!ok) continue;
+    const int64_t col = (int64_t)gs * kTileN + (lane & 15);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if (!((valid >> (rb * 4 + r)) & 1u)) continue;
+        const int64_t row = row0 + rb * 16 + 4 * (lane >> 4) + r;
+        const float s = sc[rb][r];
+        float v;
+        if constexpr (SILU)
+          v = lsilu_mul(acc[rb][j][r] * s, acc[rb][j + NSB / 2][r] * s, DT);
+        else
+          v = acc[rb][j][r] * s;
+        if constexpr (DT == kF32)
+          reinterpret_cast<float*>(p.out)[row * p.ldo + col] = v;
+        else
+          reinterpret_cast<uint16_t*>(p.out)[row * p.ldo + col] = to_dtype(v, DT);
+      }
+  }
+}
+
+// Every row's source lookup and activation scale is loaded before the first store: a load issued
+// between stores makes the wait for its value also wait for all the stores issued before it (one
+// vector-memory counter covers both), which serialized the whole epilogue.
+template <int RB, int NSB, typename SF>
+__device__ __forceinline__ void store_tile(const GemmArgs& p, const v4f (&acc)[RB][NSB], int64_t row0, int lane,
+                                           SF strip) {
+  static_assert(RB * 4 <= 32, "row mask");
+  float sc[RB][4];
+  uint32_t valid = 0;
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      int64_t ar;
+      const bool ok = lrow_source(p, row0 + rb * 16 + 4 * (lane >> 4) + r, ar);
+      sc[rb][r] = p.act_scales[ok ? ar : 0];
+      valid |= (ok ? 1u : 0u) << (rb * 4 + r);
+    }
+  if (p.out_dtype == kBF16) {
+    if (p.silu) store_tile_dt<kBF16, true>(p, acc, sc, valid, row0, lane, strip);
+    else store_tile_dt<kBF16, false>(p, acc, sc, valid, row0, lane, strip);
+  } else if (p.out_dtype == kF16) {
+    if (p.silu) store_tile_dt<kF16, true>(p, acc, sc, valid, row0, lane, strip);
+    else store_tile_dt<kF16, false>(p, acc, sc, valid, row0, lane, strip);
+  } else {
+    store_tile_dt<kF32, false>(p, acc, sc, valid, row0, lane, strip);
+  }
+}
+
 // Launch of the DMA-staged kernel (gemm_prefill_dma.hip); kErrUnsupported when it does not apply.
 int launch_prefill_dma(const GemmArgs& p, int64_t rows_to_cover, int bm_rows, hipStream_t stream);
 
