@@ -339,7 +339,13 @@ gemm_dma_kernel(const GemmArgs p) {
 
   // epilogue: lane holds rows 4*(lane>>4)+r of each row block, channel (lane & 15) of each strip
   const int64_t row0 = blk_row0 + (int64_t)wm * RB * 16;
-  store_tile(p, acc, row0, lane, [&](int j, bool& ok) __attribute__((always_inline)) { return gstrip(wn * NSB + j, ok); });
+  // the stages are free: the last step's barrier followed every wave's reads and every DMA
+  constexpr int kScr = 16 * (NSB * 16 * 4 + 16);  // one wave's row-major tile, f32 worst case
+  constexpr int kWps = kStage / kScr;
+  static_assert(3 * kWps >= NW, "epilogue scratch");
+  unsigned char* scr = (wave < kWps ? st0 : wave < 2 * kWps ? st1 : st2) + (wave % kWps) * kScr;
+  store_tile(p, acc, row0, lane, [&](int j, bool& ok) __attribute__((always_inline)) { return gstrip(wn * NSB + j, ok); },
+             scr);
 }
 
 template <int WM, int WN, int RB, int NSB, int MODE>

@@ -80,12 +80,73 @@ __device__ __forceinline__ void store_tile_dt(const GemmArgs& p, const v4f (&acc
   }
 }
 
+// The same epilogue through a per-wave LDS tile, for output rows whose stride and base are
+// 16-byte aligned: each 16-row block is written to LDS in the MFMA lane layout (2 or 4 bytes per
+// lane and element), read back row-major and stored 16 bytes per lane, so a store instruction
+// covers whole row segments (the wave's strips are contiguous columns) instead of 32-byte pieces
+// of four rows. scr: this wave's 16 * (JN*16*E + 16) bytes; nvs: the wave's strips inside N.
+template <int DT, bool SILU, int RB, int NSB>
+__device__ __forceinline__ void store_tile_lds(const GemmArgs& p, const v4f (&acc)[RB][NSB], const float (&sc)[RB][4],
+                                               uint32_t valid, int64_t row0, int lane, int64_t col0, int nvs,
+                                               unsigned char* scr) {
+  constexpr int JN = SILU ? NSB / 2 : NSB;
+  constexpr int E = DT == kF32 ? 4 : 2;
+  constexpr int W = JN * 16 * E;       // bytes of one row of the wave's tile
+  constexpr int P = W + 16;            // LDS row pitch (16-byte aligned; offsets the banks of rows 4 apart)
+  constexpr int CPR = W / 16;          // 16-byte chunks per row
+  constexpr int RPI = 64 / CPR;        // rows per store instruction (lanes past row 15 idle)
+  static_assert(CPR <= 64 && 64 % CPR == 0 && (RPI >= 16 || 16 % RPI == 0), "chunk layout");
+  const int q = lane >> 4, c = lane & 15;
+  const int crow = lane / CPR, chunk = lane % CPR;
+  const bool cok = chunk * 16 / (16 * E) < nvs;  // the chunk's strip lies inside N
+  unsigned char* outb = reinterpret_cast<unsigned char*>(p.out) + col0 * E + chunk * 16;
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float s = sc[rb][r];
+#pragma unroll
+      for (int j = 0; j < JN; ++j) {
+        float v;
+        if constexpr (SILU)
+          v = lsilu_mul(acc[rb][j][r] * s, acc[rb][j + NSB / 2][r] * s, DT);
+        else
+          v = acc[rb][j][r] * s;
+        unsigned char* d = scr + (4 * q + r) * P + j * 16 * E + c * E;
+        if constexpr (DT == kF32) *reinterpret_cast<float*>(d) = v;
+        else *reinterpret_cast<uint16_t*>(d) = to_dtype(v, DT);
+      }
+    }
+    // rows of this block that hold data: bit 4q+r from any lane of group q
+    uint32_t rv = 0;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const uint64_t b = __ballot((valid >> (rb * 4 + r)) & 1u);
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) rv |= (uint32_t)((b >> (16 * qq)) & 1u) << (4 * qq + r);
+    }
+    // LDS operations of one wave complete in order: the reads see the writes above, and the next
+    // block's writes come after these reads
+#pragma unroll
+    for (int i = 0; i < (16 + RPI - 1) / RPI; ++i) {
+      const int rr = i * RPI + crow;
+      const uint4 d = *reinterpret_cast<const uint4*>(scr + (rr < 16 ? rr : 15) * P + chunk * 16);
+      if (cok && rr < 16 && ((rv >> rr) & 1u)) {
+        const int64_t row = row0 + rb * 16 + rr;
+        *reinterpret_cast<uint4*>(outb + row * p.ldo * E) = d;
+      }
+    }
+  }
+}
+
 // Every row's source lookup and activation scale is loaded before the first store: a load issued
 // between stores makes the wait for its value also wait for all the stores issued before it (one
 // vector-memory counter covers both), which serialized the whole epilogue.
+// scr (may be null): this wave's LDS scratch for the row-major store path, at least
+// 16 * (NSB*16*4 + 16) bytes, free to overwrite.
 template <int RB, int NSB, typename SF>
 __device__ __forceinline__ void store_tile(const GemmArgs& p, const v4f (&acc)[RB][NSB], int64_t row0, int lane,
-                                           SF strip) {
+                                           SF strip, unsigned char* scr = nullptr) {
   static_assert(RB * 4 <= 32, "row mask");
   float sc[RB][4];
   uint32_t valid = 0;
@@ -98,6 +159,31 @@ __device__ __forceinline__ void store_tile(const GemmArgs& p, const v4f (&acc)[R
       sc[rb][r] = p.act_scales[ok ? ar : 0];
       valid |= (ok ? 1u : 0u) << (rb * 4 + r);
     }
+  const int esz = p.out_dtype == kF32 ? 4 : 2;
+  if (scr && ((reinterpret_cast<uintptr_t>(p.out) | (uintptr_t)(p.ldo * esz)) & 15) == 0) {
+    // the wave's strips are consecutive columns; count those inside N
+    const int jn = p.silu ? NSB / 2 : NSB;
+    int nvs = 0;
+    bool ok0;
+    const int gs0 = strip(0, ok0);
+#pragma unroll
+    for (int j = 0; j < NSB; ++j) {
+      bool ok;
+      (void)strip(j, ok);
+      nvs += (j < jn && ok) ? 1 : 0;
+    }
+    const int64_t col0 = (int64_t)gs0 * kTileN;
+    if (p.out_dtype == kBF16) {
+      if (p.silu) store_tile_lds<kBF16, true>(p, acc, sc, valid, row0, lane, col0, nvs, scr);
+      else store_tile_lds<kBF16, false>(p, acc, sc, valid, row0, lane, col0, nvs, scr);
+    } else if (p.out_dtype == kF16) {
+      if (p.silu) store_tile_lds<kF16, true>(p, acc, sc, valid, row0, lane, col0, nvs, scr);
+      else store_tile_lds<kF16, false>(p, acc, sc, valid, row0, lane, col0, nvs, scr);
+    } else {
+      store_tile_lds<kF32, false>(p, acc, sc, valid, row0, lane, col0, nvs, scr);
+    }
+    return;
+  }
   if (p.out_dtype == kBF16) {
     if (p.silu) store_tile_dt<kBF16, true>(p, acc, sc, valid, row0, lane, strip);
     else store_tile_dt<kBF16, false>(p, acc, sc, valid, row0, lane, strip);
