@@ -146,6 +146,34 @@ int w4a8_moe_gemm(const uint8_t* a_fp8, int64_t lda, const float* a_scales, int 
 int w4a8_moe_combine(const float* y, int64_t ldy, const int32_t* inv_pos, const float* topk_w, int64_t T, int top_k,
                      int64_t H, void* out, int out_dtype, void* stream);
 
+/* ---- W4A16: the same 4-bit weights against unquantized bf16/fp16 activations. */
+
+/* Exact split of bf16/fp16 rows into fp8-e4m3 terms with power-of-two scales: row t of token m
+ * (x_fp8 row T*m + t, T = 2 for bf16, 3 for fp16) holds e4m3(16^t r_t), scale 2^(E-4t), where
+ * 2^E is the smallest power of two with max|x_m| / 2^E <= 448, r_0 = x / 2^E and
+ * r_{t+1} = 16 r_t - e4m3(r_t); x = sum_t scale_t * code_t exactly for scaled magnitudes of at
+ * least 2^-6. No counterpart in the reference (whose W4A16 kernels read x directly); it is the
+ * activation side of w4a16_linear, exposed for testing and for callers that run the GEMM
+ * themselves. x rows 16-byte aligned, K % 8 == 0; x_fp8 rows 8-byte aligned. */
+int w4a16_act_split(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, uint8_t* x_fp8, int64_t ldq,
+                    float* scales, void* stream);
+
+/* Workspace of w4a16_linear: the split rows (T*M x K rounded to 16), their scales and the terms'
+ * f32 GEMM rows (T*M x N); -1 on bad sizes. */
+int64_t w4a16_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int x_dtype);
+
+/* Dense W4A16 linear: y = x @ W^T with x never rounded (f32 accumulation), out in x's dtype, same
+ * weights and scale formats as w4a8_gemm (int4 with fp16 group scales and optional zeros, e2m1 with
+ * E8M0 or fp16 scales). silu != 0: the fused gate_up arm, out (M, N/2) = silu(gate) * up with gate
+ * and up rounded to the dtype first. Replaces fp8_wmma.mmq_regdirect_w4a16_gemv /
+ * mmq_w4a16_tiled / mmq_regdirect_w4a16_gemv_silu (python/minisgl/quant/kernels.py:1125-1178,
+ * 1756-1786): the kernel arm follows M (decode GEMV up to 16 tokens, the tiled GEMM above), the
+ * activations go through w4a16_act_split and the W4A8 GEMM, and one sum kernel adds each token's
+ * terms in order and rounds once. */
+int w4a16_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const void* w_tile, int64_t N,
+                 const void* scales, int scale_fmt, const int32_t* zeros, int wfmt, int64_t group_size, void* out,
+                 int64_t ldo, int silu, void* workspace, int64_t workspace_bytes, int kernel, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

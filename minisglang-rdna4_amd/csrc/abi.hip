@@ -27,6 +27,10 @@ bool moe_prep_fits(int64_t T, int top_k);
 int launch_rms_norm(const void* x, int64_t ldx, void* res, int64_t ldr, const void* weight, int plus_one, float eps,
                     int64_t M, int64_t K, int dtype, void* out, int64_t ldo, uint8_t* q, int64_t ldq, float* scales,
                     hipStream_t stream);
+int w4a16_terms(int dtype);
+int launch_act_split(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx, uint8_t* q, int64_t ldq,
+                     float* scales, hipStream_t stream);
+int launch_tsum(const float* y, int64_t N, int64_t M, int dtype, void* out, int64_t ldo, int silu, hipStream_t st);
 int launch_moe_prep(const void* logits, int ldtype, int64_t T, int E, int top_k, int renorm, float* tw,
                     int32_t* ids, int bm, int64_t P, int32_t* sorted_ids, int32_t* expert_ids, int32_t* ntp,
                     int32_t* inv_pos, const void* x, int xdtype, int64_t K, int64_t ldx, uint8_t* xq, int64_t ldq,
@@ -230,6 +234,74 @@ int w4a8_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, c
   p.xq = xq; p.ldx = K; p.act_scales = xs;
   return run_dense("w4a8_linear", p, kernel, st);
 }
+
+// ---- W4A16: unquantized bf16/fp16 activations, split exactly into fp8 terms (w4a16.hip)
+static int64_t round16(int64_t b) { return (b + 15) / 16 * 16; }
+
+extern "C" {
+
+int64_t w4a16_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int x_dtype) {
+  if (M < 0 || N <= 0 || K <= 0 || (x_dtype != kBF16 && x_dtype != kF16)) return -1;
+  const int64_t T = w4a16_terms(x_dtype);
+  return round256(T * M * round16(K)) + round256(T * M * 4) + round256(T * M * N * 4);
+}
+
+int w4a16_act_split(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, uint8_t* x_fp8, int64_t ldq,
+                    float* scales, void* stream) {
+  if (x_dtype != kBF16 && x_dtype != kF16) return fail(kErrInvalid, "w4a16_act_split: x must be bf16 or fp16");
+  if (M < 0 || K <= 0 || K % 8) return fail(kErrInvalid, "w4a16_act_split: K=%lld must be a positive multiple of 8", (long long)K);
+  if (ldx < K || ldx % 8 || !aligned16(x))
+    return fail(kErrInvalid, "w4a16_act_split: x rows must be 16-byte aligned with stride >= K (ldx=%lld)", (long long)ldx);
+  if (ldq < K || ldq % 8 || (reinterpret_cast<uintptr_t>(x_fp8) & 7u) || !scales)
+    return fail(kErrInvalid, "w4a16_act_split: x_fp8 rows must be 8-byte aligned with stride >= K (ldq=%lld), scales non-null",
+                (long long)ldq);
+  return hip_status(launch_act_split(x, x_dtype, M, K, ldx, x_fp8, ldq, scales, (hipStream_t)stream), "w4a16_act_split");
+}
+
+int w4a16_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const void* w_tile, int64_t N,
+                 const void* scales, int scale_fmt, const int32_t* zeros, int wfmt, int64_t group_size, void* out,
+                 int64_t ldo, int silu, void* workspace, int64_t workspace_bytes, int kernel, void* stream) {
+  GemmArgs p;
+  // the GEMM writes the terms' f32 rows into the workspace (out set below); the sum kernel
+  // rounds, and applies silu * up for the fused arm
+  int rc = dense_args("w4a16_linear", M, w_tile, N, K, scales, scale_fmt, zeros, wfmt, group_size, workspace, kF32, N, 0,
+                      kernel, p);
+  if (rc) return rc;
+  if (x_dtype != kBF16 && x_dtype != kF16) return fail(kErrInvalid, "w4a16_linear: x must be bf16 or fp16 (dtype %d)", x_dtype);
+  if (silu && (N % 32)) return fail(kErrInvalid, "w4a16_linear: fused silu needs N=2*inter with inter %% 16 == 0 (N=%lld)", (long long)N);
+  const int64_t nout = silu ? N / 2 : N;
+  if (ldo < nout) return fail(kErrInvalid, "w4a16_linear: ldo=%lld < output width %lld", (long long)ldo, (long long)nout);
+  if (M == 0) return kOk;
+  if (K % 8 || ldx < K || ldx % 8 || !aligned16(x))
+    return fail(kErrInvalid, "w4a16_linear: x rows must be 16-byte aligned with stride >= K, K %% 8 == 0 (ldx=%lld)", (long long)ldx);
+  const int64_t need = w4a16_linear_workspace_bytes(M, N, K, x_dtype);
+  if (workspace == nullptr || workspace_bytes < need || !aligned16(workspace))
+    return fail(kErrInvalid, "w4a16_linear: needs a 16-byte aligned workspace of %lld bytes, got %lld", (long long)need,
+                (long long)workspace_bytes);
+  const hipStream_t st = (hipStream_t)stream;
+  const int64_t T = w4a16_terms(x_dtype), ldq = round16(K);
+  uint8_t* xq = reinterpret_cast<uint8_t*>(workspace);
+  float* xs = reinterpret_cast<float*>(xq + round256(T * M * ldq));
+  float* y = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(xs) + round256(T * M * 4));
+  rc = launch_act_split(x, x_dtype, M, K, ldx, xq, ldq, xs, st);
+  if (rc) return hip_status(rc, "w4a16_linear(act split)");
+  p.M = T * M;
+  p.xq = xq; p.ldx = ldq; p.act_scales = xs;
+  p.out = y; p.ldo = N;
+  // the kernel choice follows the token count, as the reference's arm does
+  const bool decode = kernel == 1 || (kernel == 0 && M <= kGemvMaxRows);
+  if (decode) {
+    rc = hip_status(launch_gemv(p, (p.M + 15) / 16, false, st), "w4a16_linear(decode)");
+  } else {
+    rc = launch_prefill_lds(p, p.M, 0, st);
+    if (rc == kErrUnsupported) rc = launch_prefill(p, p.M, 128, st);
+    rc = hip_status(rc, "w4a16_linear(prefill)");
+  }
+  if (rc) return rc;
+  return hip_status(launch_tsum(y, N, M, x_dtype, out, ldo, silu, st), "w4a16_linear(sum)");
+}
+
+}  // extern "C"
 
 static int check_route(const char* who, int logits_dtype, int64_t E, int top_k) {
   if (logits_dtype != kBF16 && logits_dtype != kF16 && logits_dtype != kF32)

@@ -229,6 +229,28 @@ def _check_producer_pair(x: torch.Tensor, x_fp8, act_scales, what: str):
     return xq, act_scales.contiguous()
 
 
+def _dense_prep(x, w_packed, scales, w_zeros, group_size, weight_is_e2m1, what):
+    """Shape/dtype checks shared by the dense arms; returns (M, K, N, sfmt, w_zeros, tiles)."""
+    if x.dim() != 2 or x.dtype not in (torch.bfloat16, torch.float16):
+        raise TypeError(f"{what}: x must be 2-D bf16/fp16, got {x.dtype} {tuple(x.shape)}")
+    M, K = x.shape
+    N = _n_of(w_packed)
+    G = K // group_size
+    if K % group_size or tuple(scales.shape) != (G, N):
+        raise AssertionError(f"{what}: scales must be GROUP-major (K//group, N)=({G}, {N}), got "
+                             f"{tuple(scales.shape)}")
+    sfmt = _scale_fmt(scales, weight_is_e2m1, what)
+    if weight_is_e2m1 and w_zeros is not None and w_zeros.numel() > 0:
+        raise AssertionError(f"{what}: e2m1 weights are symmetric; w_zeros must be None")
+    if w_zeros is not None and w_zeros.numel() == 0:
+        w_zeros = None
+    if w_zeros is not None and (w_zeros.dtype != torch.int32 or tuple(w_zeros.shape) != (G, N // 8)):
+        raise AssertionError(f"{what}: w_zeros must be (K//group, N/8)=({G}, {N // 8}) int32, got "
+                             f"{w_zeros.dtype} {tuple(w_zeros.shape)}")
+    tiles = _as_tiles(w_packed, K, weight_is_e2m1, 2, what)
+    return M, K, N, sfmt, w_zeros, tiles
+
+
 def _dense(x, w_packed, scales, w_zeros, group_size, weight_is_e2m1, x_fp8, act_scales, silu, arm):
     what = "w4a8_linear_silu" if silu else "w4a8_linear"
     if x.dim() != 2 or x.dtype not in (torch.bfloat16, torch.float16):
@@ -333,6 +355,84 @@ def w4a8_linear_silu(
 # --------------------------------------------------------------------------------------------
 # MoE
 # --------------------------------------------------------------------------------------------
+def _w4a16(x, w_packed, scales, w_zeros, group_size, weight_is_e2m1, silu, what):
+    M, K, N, sfmt, w_zeros, tiles = _dense_prep(x, w_packed, scales, w_zeros, group_size, weight_is_e2m1, what)
+    if K % 8:
+        raise AssertionError(f"{what}: K={K} must be a multiple of 8")
+    kernel = _pick_dense_kernel(M, weight_is_e2m1, group_size, k=K, n=N)
+    arm = _abi.KERNEL_DECODE if kernel == "decode_gemv" else _abi.KERNEL_PREFILL
+    nout = N // 2 if silu else N
+    x = x.contiguous()
+    out = torch.empty((M, nout), dtype=x.dtype, device=x.device)
+    lib = _abi.load()
+    ws_bytes = int(lib.w4a16_linear_workspace_bytes(M, N, K, _abi.dtype_code(x.dtype)))
+    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=x.device)
+    zeros = _abi.ptr(w_zeros.contiguous() if w_zeros is not None else None)
+    wfmt = _abi.W_E2M1 if weight_is_e2m1 else _abi.W_INT4
+    _abi.check(
+        lib.w4a16_linear(_abi.ptr(x), _abi.dtype_code(x.dtype), M, K, K, _abi.ptr(tiles), N,
+                         _abi.ptr(scales.contiguous()), sfmt, zeros, wfmt, group_size, _abi.ptr(out), nout,
+                         int(silu), _abi.ptr(ws), ws_bytes, arm, _abi.stream_of(x)),
+        what,
+    )
+    return out, kernel
+
+
+def w4a16_linear(
+    x: torch.Tensor,  # (M, K) bf16/fp16 activations, never quantized
+    w_packed: torch.Tensor,  # (N, K/8) int32 op layout, or W4 tiles (the same weights the W4A8 arms take)
+    scales: torch.Tensor,  # (K/group, N) fp16 group-major, or uint8 E8M0 (e2m1 only)
+    w_zeros: torch.Tensor | None,  # (K/group, N/8) int32 (asymmetric) or None
+    group_size: int,
+    N: int,
+    weight_is_e2m1: bool = False,
+) -> torch.Tensor:
+    """Dense W4A16 GEMM (python/minisgl/quant/kernels.py:1125-1178): (M, K) @ (N, K)^T in x's dtype
+    with the activations unquantized. The arm follows M as in the reference (decode GEMV up to 16
+    tokens, the tiled GEMM above); both take the W4A8 weights as they are. The activations enter the
+    fp8 MFMA kernels through an exact split into fp8 terms (two for bf16, three for fp16) whose f32
+    partial results are summed per token before the one rounding to the output dtype."""
+    if _n_of(w_packed) != N:
+        raise AssertionError(f"w4a16_linear: N={N} does not match the weight's {_n_of(w_packed)} rows")
+    out, kernel = _w4a16(x, w_packed, scales, w_zeros, group_size, weight_is_e2m1, False, "w4a16_linear")
+    engaged(f"w4a8_mi355x.w4a16_{'gemv' if kernel == 'decode_gemv' else 'tiled'}"
+            f"{'+e2m1' if weight_is_e2m1 else ''}")
+    return out
+
+
+def w4a16_linear_silu(
+    x: torch.Tensor,
+    w_packed: torch.Tensor,  # (2*inter, K/8) [gate | up]
+    scales: torch.Tensor,
+    w_zeros: torch.Tensor | None,
+    group_size: int,
+    weight_is_e2m1: bool = False,
+) -> torch.Tensor:
+    """Fused gate_up W4A16 + silu_and_mul -> (M, inter) (python/minisgl/quant/kernels.py:1756-1786):
+    gate and up are the w4a16_linear outputs rounded to the dtype, then silu(gate) in f32, rounded,
+    times up, rounded; bit-identical to w4a16_linear followed by that silu_mul."""
+    out, kernel = _w4a16(x, w_packed, scales, w_zeros, group_size, weight_is_e2m1, True, "w4a16_linear_silu")
+    engaged(f"w4a8_mi355x.w4a16_{'gemv' if kernel == 'decode_gemv' else 'tiled'}_silu"
+            f"{'+e2m1' if weight_is_e2m1 else ''}")
+    return out
+
+
+def w4a16_act_split(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """The activation side of the W4A16 arm: (T*M, K) uint8 e4m3 codes and (T*M,) f32 power-of-two
+    scales with x[m] == sum_t scales[T*m+t] * e4m3(codes[T*m+t]) (T = 2 for bf16, 3 for fp16)."""
+    if x.dim() != 2 or x.dtype not in (torch.bfloat16, torch.float16) or x.shape[1] % 8:
+        raise TypeError(f"w4a16_act_split: x must be 2-D bf16/fp16 with K % 8 == 0, got {x.dtype} {tuple(x.shape)}")
+    x = x.contiguous()
+    M, K = x.shape
+    T = 2 if x.dtype == torch.bfloat16 else 3
+    q = torch.empty((T * M, K), dtype=torch.uint8, device=x.device)
+    s = torch.empty((T * M,), dtype=torch.float32, device=x.device)
+    lib = _abi.load()
+    _abi.check(lib.w4a16_act_split(_abi.ptr(x), _abi.dtype_code(x.dtype), M, K, K, _abi.ptr(q), K, _abi.ptr(s),
+                                   _abi.stream_of(x)), "w4a16_act_split")
+    return q, s
+
+
 def _moe_block_m(num_tokens: int, num_experts: int, top_k: int, flag_gemm1: bool | None = None) -> int:
     """Grouped-GEMM tile height from the workload (python/minisgl/quant/kernels.py:355-420): the
     largest of 16/32/64/128 not above the mean rows per expert; past the gemm1 GEMV crossover

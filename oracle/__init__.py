@@ -58,6 +58,8 @@ def lib() -> ctypes.CDLL:
                                       vp, vp, vp, vp, vp, vp, ci, ci, i64, i64, vp, vp]
         L.w4o_rms_norm.restype = None
         L.w4o_rms_norm.argtypes = [vp, vp, vp, ci, f, ci, i64, i64, vp]
+        L.w4o_act_split.restype = None
+        L.w4o_act_split.argtypes = [vp, ci, i64, i64, vp, vp]
         L.w4o_silu_mul.restype = ctypes.c_uint16
         L.w4o_silu_mul.argtypes = [ctypes.c_double, ctypes.c_double, ci]
         L.w4o_bf16_to_f32.restype = f
@@ -208,3 +210,27 @@ def rms_norm(x_bits: np.ndarray, weight_bits: np.ndarray | None, eps: float, dty
     w = None if weight_bits is None else np.ascontiguousarray(weight_bits, dtype=np.uint16)
     lib().w4o_rms_norm(_p(x), _p(res), _p(w), int(plus_one), float(eps), dtype, M, K, _p(out))
     return out, res
+
+
+def act_split(x_bits: np.ndarray, dtype: int = 0) -> tuple[np.ndarray, np.ndarray]:
+    """W4A16 activation split of (M, K) bf16 (dtype 0) / fp16 (dtype 1) bit patterns -> (codes (T*M, K)
+    u8, scales (T*M,) f32), T = 2 for bf16, 3 for fp16."""
+    x = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    M, K = x.shape
+    T = 2 if dtype == 0 else 3
+    q = np.empty((T * M, K), dtype=np.uint8)
+    s = np.empty((T * M,), dtype=np.float32)
+    lib().w4o_act_split(_p(x), dtype, M, K, _p(q), _p(s))
+    return q, s
+
+
+def w4a16_gemm(x_bits: np.ndarray, dtype: int, w_packed: np.ndarray, scales: np.ndarray, zeros: np.ndarray | None,
+               group: int, e2m1: bool = False) -> np.ndarray:
+    """f64 y = x @ dequant(W)^T with x decoded exactly from its bf16/fp16 bits (the unquantized
+    activations of python/minisgl/quant/kernels.py:1125-1178)."""
+    xb = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    if dtype == 0:
+        x = bf16_to_f32(xb).astype(np.float64)
+    else:
+        x = xb.view(np.float16).astype(np.float64)
+    return x @ dequant(w_packed, scales, zeros, group, e2m1).T

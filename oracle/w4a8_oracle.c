@@ -21,6 +21,10 @@
  *   gemm            -- brute force on tiny inputs against a dequantize-then-matmul numpy path,
  *                      and the invariants M-invariance / row-split / linearity in the weights.
  *   moe align       -- the worked example in python/minisgl/moe/fused.py:80-97.
+ *   w4a16 split     -- the identity x == sum_t scale_t * e4m3(code_t) (exact for every bf16 value
+ *                      and every fp16 value whose scaled magnitude is >= 2^-6), the scale being the
+ *                      smallest power of two with amax/scale <= 448 (checked against frexp), and
+ *                      each term's code being the RNE e4m3 of its residual (torch's cast).
  */
 #include <math.h>
 #include <stdint.h>
@@ -450,4 +454,40 @@ void w4o_rms_norm(const uint16_t* x, uint16_t* residual, const uint16_t* weight,
     }
   }
   free(row);
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* W4A16 activation split. The reference's W4A16 arm (python/minisgl/quant/kernels.py:1125-1178) */
+/* reads bf16/fp16 x unrounded; this build feeds the fp8 GEMM an exact fp8 expansion of x:       */
+/* T terms (2 for bf16, 3 for fp16), term t = e4m3(r_t) with r_0 = x / 2^E,                      */
+/* r_{t+1} = 16 (r_t - e4m3(r_t)), scale 2^(E - 4t), 2^E the smallest power of two with          */
+/* amax / 2^E <= 448 (E = 0 for a zero row). Rows of token m are T*m + t.                        */
+/* ------------------------------------------------------------------------------------------ */
+static int split_exponent(float amax) {
+  if (!(amax > 0.0f)) return 0;
+  int e;
+  const float m = 2.0f * frexpf(amax, &e);
+  e -= 1;
+  return m <= 1.75f ? e - 8 : e - 7;
+}
+
+void w4o_act_split(const uint16_t* x, int dtype, int64_t M, int64_t K, uint8_t* q, float* scales) {
+  const int T = dtype == 0 ? 2 : 3;
+  for (int64_t m = 0; m < M; ++m) {
+    float amax = 0.0f;
+    for (int64_t k = 0; k < K; ++k) {
+      const float v = fabsf(dtype == 0 ? w4o_bf16_to_f32(x[m * K + k]) : w4o_f16_to_f32(x[m * K + k]));
+      amax = v > amax ? v : amax;
+    }
+    const int E = split_exponent(amax);
+    for (int64_t k = 0; k < K; ++k) {
+      float r = ldexpf(dtype == 0 ? w4o_bf16_to_f32(x[m * K + k]) : w4o_f16_to_f32(x[m * K + k]), -E);
+      for (int t = 0; t < T; ++t) {
+        const uint8_t c = w4o_f32_to_e4m3(r);
+        q[(T * m + t) * K + k] = c;
+        r = (r - w4o_e4m3_to_f32(c)) * 16.0f;
+      }
+    }
+    for (int t = 0; t < T; ++t) scales[T * m + t] = ldexpf(1.0f, E - 4 * t);
+  }
 }

@@ -13,7 +13,7 @@ HEADER = REPO / "include" / "w4a8_mi355x.h"
 
 def _declared() -> list[str]:
     text = HEADER.read_text()
-    return sorted(set(re.findall(r"^[A-Za-z_][\w\s\*]*?\b(w4a8_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^[A-Za-z_][\w\s\*]*?\b(w4a(?:8|16)_\w+)\s*\(", text, re.M)))
 
 
 @pytest.fixture(scope="module")
@@ -39,7 +39,7 @@ def _declared_params() -> dict[str, list[str]]:
     """name -> parameter type list, parsed from the header's prototypes."""
     text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
     out = {}
-    for m in re.finditer(r"^[A-Za-z_][\w\s\*]*?\b(w4a8_\w+)\s*\(([^)]*)\)\s*;", text, re.M):
+    for m in re.finditer(r"^[A-Za-z_][\w\s\*]*?\b(w4a(?:8|16)_\w+)\s*\(([^)]*)\)\s*;", text, re.M):
         params = [p.strip() for p in m.group(2).replace("\n", " ").split(",") if p.strip()]
         if params == ["void"]:
             params = []

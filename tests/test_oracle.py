@@ -345,3 +345,72 @@ def test_rms_norm_add_residual_is_dtype_sum(oracle):
         assert torch.equal(_from_bits(nr, dtype), x + r)
         o2, _ = oracle.rms_norm(_bits(x + r), _bits(w), 1e-5, code, False)
         assert np.array_equal(o, o2)
+
+
+# ------------------------------------------------------------------------------- w4a16 split
+def _split_recon(codes: np.ndarray, scales: np.ndarray, T: int) -> np.ndarray:
+    dec = torch.from_numpy(codes).view(torch.float8_e4m3fn).to(torch.float64).numpy()
+    v = (dec * scales.astype(np.float64)[:, None]).reshape(-1, T, codes.shape[1]).sum(axis=1)
+    return v
+
+
+@pytest.mark.parametrize("dtype,code,T", [(torch.bfloat16, 0, 2), (torch.float16, 1, 3)])
+def test_w4a16_split_is_exact(oracle, dtype, code, T):
+    """x == sum_t scale_t * e4m3(code_t) exactly, on random rows with outliers and on edge rows
+    (all zero, one nonzero, amax exactly 448 * 2^j and just above, mixed binades)."""
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(6, 512, generator=g) * torch.logspace(-3, 3, 6)[:, None]
+    x[0] = 0.0
+    x[1] = 0.0
+    x[1, 17] = -3.25
+    x[2, :] = torch.linspace(-448.0, 448.0, 512)
+    x[3, :] = torch.linspace(-1.0, 1.0, 512) * 449.0
+    x[4, ::3] *= 50.0
+    xb = x.to(dtype)
+    bits = xb.view(torch.int16).numpy().view(np.uint16)
+    q, s = oracle.act_split(bits, code)
+    assert q.shape == (T * 6, 512) and s.shape == (T * 6,)
+    # the scale: smallest power of two with amax / scale <= 448
+    xs = xb.float().numpy().astype(np.float64)
+    for m in range(6):
+        amax = np.abs(xs[m]).max()
+        s0 = float(s[T * m])
+        if amax == 0:
+            assert s0 == 1.0
+            continue
+        assert np.log2(s0) == np.round(np.log2(s0))
+        assert amax / s0 <= 448.0 < amax / (s0 / 2)
+        assert all(s[T * m + t] == s0 * 16.0 ** -t for t in range(T))
+    rec = _split_recon(q, s, T)
+    small = np.abs(xs) < np.repeat(s[::T].astype(np.float64)[:, None], 512, axis=1) * 2.0 ** -6
+    assert np.array_equal(rec[~small], xs[~small])
+    # below 2^-6 of the scale the subnormal terms keep an absolute error under 2^(E-13)
+    assert np.all(np.abs(rec - xs)[small] <= np.repeat(s[::T].astype(np.float64)[:, None], 512, axis=1)[small] * 2.0 ** -13)
+
+
+def test_w4a16_split_terms_are_rne_of_the_residual(oracle):
+    """Each code is torch's RNE e4m3 cast of its residual, the residual recomputed in f32."""
+    g = torch.Generator().manual_seed(8)
+    x = (torch.randn(3, 256, generator=g) * 5).to(torch.float16)
+    q, s = oracle.act_split(x.view(torch.int16).numpy().view(np.uint16), 1)
+    for m in range(3):
+        r = (x[m].float() / float(s[3 * m])).numpy()
+        for t in range(3):
+            assert np.array_equal(q[3 * m + t], _torch_e4m3(r))
+            r = ((r - torch.from_numpy(q[3 * m + t]).view(torch.float8_e4m3fn).float().numpy()) * 16.0).astype(np.float32)
+
+
+def test_w4a16_gemm_reference_brute_force(oracle):
+    """The W4A16 reference is x @ dequant(W)^T: brute force on a tiny case."""
+    N, K, g = 16, 64, 32
+    w, sc, z = synth.int4_weight(N, K, g, seed=3, asym=True)
+    x = (torch.randn(2, K, generator=torch.Generator().manual_seed(4))).to(torch.bfloat16)
+    ref = oracle.w4a16_gemm(x.view(torch.int16).numpy().view(np.uint16), 0, w.numpy(), sc.numpy(), z.numpy(), g)
+    codes = ((w.numpy()[:, :, None] >> (4 * np.arange(8))) & 15).reshape(N, K).astype(np.float64)
+    zz = ((z.numpy()[:, :, None] >> (4 * np.arange(8))) & 15).reshape(K // g, N).astype(np.float64)
+    s64 = sc.numpy().astype(np.float64)
+    want = np.zeros((2, N))
+    for m in range(2):
+        for n in range(N):
+            want[m, n] = sum(float(x[m, k]) * (codes[n, k] - zz[k // g, n]) * s64[k // g, n] for k in range(K))
+    assert np.allclose(ref, want, rtol=1e-12, atol=1e-12)
