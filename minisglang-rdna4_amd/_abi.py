@@ -14,7 +14,7 @@ _PKG = Path(__file__).resolve().parent
 _LIB_PATH = _PKG / "_lib" / "libw4a8_mi355x.so"
 
 BF16, F16, F32 = 0, 1, 2
-SCALE_F16, SCALE_E8M0 = 0, 1
+SCALE_F16, SCALE_E8M0, SCALE_E4M3 = 0, 1, 2
 W_INT4, W_E2M1 = 0, 1
 KERNEL_AUTO, KERNEL_DECODE, KERNEL_PREFILL = 0, 1, 2
 

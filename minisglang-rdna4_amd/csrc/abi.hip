@@ -73,12 +73,19 @@ static int check_weights(const char* who, int64_t N, int64_t K, int scale_fmt, c
   if (N % 16) return fail(kErrInvalid, "%s: N=%lld must be a multiple of 16", who, (long long)N);
   if (K % 32) return fail(kErrInvalid, "%s: K=%lld must be a multiple of 32", who, (long long)K);
   if (wfmt != kInt4 && wfmt != kE2M1) return fail(kErrInvalid, "%s: unknown weight format %d", who, wfmt);
-  if (scale_fmt != kScaleF16 && scale_fmt != kScaleE8M0)
+  if (scale_fmt != kScaleF16 && scale_fmt != kScaleE8M0 && scale_fmt != kScaleE4M3)
     return fail(kErrInvalid, "%s: unknown scale format %d", who, scale_fmt);
-  if (!(group == 32 || group == 64 || (group >= 128 && (group & (group - 1)) == 0)))
-    return fail(kErrUnsupported, "%s: group_size=%lld unsupported (32, 64 or a power of two >= 128)", who, (long long)group);
+  // 16-wide groups: NVFP4 (e4m3 block scales) and e2m1 with fp16 group scales
+  const bool g16 = group == 16 && wfmt == kE2M1;
+  if (!(g16 || group == 32 || group == 64 || (group >= 128 && (group & (group - 1)) == 0)))
+    return fail(kErrUnsupported, "%s: group_size=%lld unsupported (32, 64 or a power of two >= 128; 16 for e2m1)", who,
+                (long long)group);
   if (K % group) return fail(kErrInvalid, "%s: K=%lld is not a multiple of group_size=%lld", who, (long long)K, (long long)group);
-  if (wfmt == kE2M1 && zeros) return fail(kErrInvalid, "%s: e2m1 weights are symmetric; w_zeros must be empty", who);
+  if (scale_fmt == kScaleE4M3 && (wfmt != kE2M1 || !zeros))
+    return fail(kErrInvalid, "%s: e4m3 (NVFP4) block scales need e2m1 weights and the per-output-channel f32 global "
+                "in the zeros slot", who);
+  if (wfmt == kE2M1 && zeros && scale_fmt != kScaleE4M3)
+    return fail(kErrInvalid, "%s: e2m1 weights are symmetric; w_zeros must be empty (it carries only the NVFP4 global)", who);
   if (scale_fmt == kScaleE8M0 && wfmt != kE2M1)
     return fail(kErrInvalid, "%s: E8M0 (uint8) scales are only defined for e2m1 weights", who);
   if (scale_fmt == kScaleE8M0 && group != 32)
@@ -401,7 +408,8 @@ int w4a8_moe_gemm(const uint8_t* a_fp8, int64_t lda, const float* a_scales, int 
   p.bm = block_m; p.a_by_token = a_by_token;
   p.w_expert_tiles = (N / 16) * p.KT;
   p.s_expert_stride = (K / group_size) * N;
-  p.z_expert_stride = (K / group_size) * (N / 8);
+  // the NVFP4 global is one f32 per output channel per expert; zero words are (K/g, N/8) per expert
+  p.z_expert_stride = scale_fmt == kScaleE4M3 ? N : (K / group_size) * (N / 8);
   p.out = out; p.out_dtype = out_dtype; p.ldo = ldo; p.silu = silu;
   const int64_t nblk = moe_max_blocks(numel, E, block_m, P);
   if (decode) {

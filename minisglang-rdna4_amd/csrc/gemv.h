@@ -112,6 +112,7 @@ __device__ __forceinline__ void gemv_tile(const GemmArgs& p, const v8i& a, const
     for (int ss = 0; ss < GPT; ++ss)
       rh[ss] = GPT == 1 ? mfma_f8f8(a, half8, zero4) : mfma_f8f8_sb(a, half8, zero4, subgroup_mask_scale(lane, GPT, ss));
   }
+  static_assert(GPT < 8 || WFMT == kE2M1, "16-wide groups are e2m1 only");
 #pragma unroll
   for (int j = 0; j < NSTR; ++j) {
     if (!sval[j]) continue;
@@ -120,11 +121,12 @@ __device__ __forceinline__ void gemv_tile(const GemmArgs& p, const v8i& a, const
 #pragma unroll
     for (int ss = 0; ss < GPT; ++ss) {
       const int msk = GPT == 1 ? 127 : subgroup_mask_scale(lane, GPT, ss);
-      const v4f c = WFMT == kInt4 ? mfma_f8f8_sb(a, b, zero4, msk) : mfma_f8f4_sb(a, b, zero4, msk);
+      const v4f c = WFMT == kInt4 ? mfma_f8f8_sb(a, b, zero4, msk)
+                                  : mfma_f8f4_sb(a, GPT == 8 ? fp4_half_operand(b, ss) : b, zero4, msk);
       const bool in = kbase + ss * kSub < K;
       int g = (kbase + ss * kSub) / group;
       g = g < ngroups ? g : ngroups - 1;
-      const float sc = in ? load_scale(scales, p.sfmt, (int64_t)g * N + n) : 0.0f;
+      const float sc = in ? group_scale(scales, p.sfmt, (int64_t)g * N + n, zeros, n) : 0.0f;
       if (WFMT == kInt4) {
         float coef = -1.0f;
         if (!SYM) {
@@ -211,7 +213,7 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemmArgs p, int tpw) {
   const uint4* wt = p.wt + (size_t)(expert * p.w_expert_tiles) * 64;
   // scale element size from the mode (E8M0 bytes, else fp16), so that the scale base stays in
   // scalar registers
-  constexpr int kEsz = MODE == kModeE8M0 ? 1 : 2;
+  const int kEsz = (MODE == kModeE8M0 || (MODE == kModeE2M1F16 && p.sfmt == kScaleE4M3)) ? 1 : 2;
   const void* scales = reinterpret_cast<const char*>(p.scales) + (size_t)(expert * p.s_expert_stride) * kEsz;
   const int32_t* zeros = p.zeros ? p.zeros + expert * p.z_expert_stride : nullptr;
   // 32-bit index math on the hot path (tile, scale and zero indices of one matrix fit easily)

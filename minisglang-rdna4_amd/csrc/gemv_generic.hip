@@ -1,5 +1,5 @@
-// Decode GEMV launch unit for the sub-tile-group formats: int4 with group 32/64 and e2m1 with fp16
-// group scales (kernel template in gemv.h). Groups per tile are a template constant so the
+// Decode GEMV launch unit for the sub-tile-group formats: int4 with group 32/64, e2m1 with fp16
+// group scales and NVFP4 (e2m1 with e4m3 group-16 scales and a per-channel global) (kernel template in gemv.h). Groups per tile are a template constant so the
 // per-tile sub-group loop is straight-line code.
 #include "gemv.h"
 
@@ -8,6 +8,12 @@ namespace w4a8 {
 template <int NS, int CHK, int MD, bool SY>
 static void launch_gpt(const GemmArgs& p, dim3 grid, dim3 block, size_t lds, int tpw, hipStream_t stream) {
   const int gpt = p.group >= kTileK ? 1 : kTileK / p.group;
+  if constexpr (MD == kModeE2M1F16) {
+    if (gpt == 8) {
+      hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, kAGlobal, SY, 4, 8>), grid, block, lds, stream, p, tpw);
+      return;
+    }
+  }
   if (gpt == 4)
     hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, kAGlobal, SY, 4, 4>), grid, block, lds, stream, p, tpw);
   else if (gpt == 2)

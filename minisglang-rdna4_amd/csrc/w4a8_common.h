@@ -42,7 +42,9 @@ constexpr int kErrUnsupported = 2;
 constexpr int kErrHip = 3;
 
 enum DType { kBF16 = 0, kF16 = 1, kF32 = 2 };
-enum ScaleFmt { kScaleF16 = 0, kScaleE8M0 = 1 };
+// kScaleE4M3: NVFP4's e4m3 block scales (group 16), times a per-output-channel f32 global that
+// rides the zeros slot (e2m1 weights have no zero points)
+enum ScaleFmt { kScaleF16 = 0, kScaleE8M0 = 1, kScaleE4M3 = 2 };
 enum WFmt { kInt4 = 0, kE2M1 = 1 };
 
 // e4m3 constants
@@ -276,14 +278,31 @@ __device__ __forceinline__ v8i load_a_operand(const uint8_t* row, int kvalid, in
 // i.e. far below one f32 ulp of any accumulated value) outside it.
 __device__ __forceinline__ int subgroup_mask_scale(int lane, int gpt, int sg) {
   const int blk = lane >> 4;           // K block (32 wide) the lane's scale governs
+  if (gpt == 8) return (blk == (sg >> 1)) ? 127 : 0;  // 16-wide groups: half a block each
   const int per = 4 / gpt;             // blocks per sub-group
   return (blk / per == sg) ? 127 : 0;
+}
+
+// 16-wide sub-group sg of an e2m1 operand (8 groups per 128-element tile): a lane's 16 bytes hold
+// its block's elements 0..31 in order, two per byte, so the other half of the block is zeroed
+__device__ __forceinline__ v8i fp4_half_operand(const v8i& b, int sg) {
+  v8i h = b;
+  if (sg & 1) { h[0] = 0; h[1] = 0; }
+  else { h[2] = 0; h[3] = 0; }
+  return h;
 }
 
 __device__ __forceinline__ float load_scale(const void* scales, int fmt, int64_t idx) {
   if (fmt == kScaleF16) return f16_to_f32(reinterpret_cast<const uint16_t*>(scales)[idx]);
   uint32_t s = reinterpret_cast<const uint8_t*>(scales)[idx];
+  if (fmt == kScaleE4M3) return __builtin_amdgcn_cvt_f32_fp8((int)s, 0);
   return s == 0 ? 5.877471754111438e-39f : __uint_as_float(s << 23);
+}
+
+// group scale of output channel n: the stored scale, times the NVFP4 global (zeros slot, f32 bits)
+__device__ __forceinline__ float group_scale(const void* scales, int fmt, int64_t idx, const int32_t* zeros, int64_t n) {
+  const float s = load_scale(scales, fmt, idx);
+  return fmt == kScaleE4M3 ? s * __int_as_float(zeros[n]) : s;
 }
 
 }  // namespace w4a8

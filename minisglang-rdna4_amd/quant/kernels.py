@@ -202,14 +202,33 @@ def _pick_dense_kernel(m: int, weight_is_e2m1: bool = False, group_size: int = 1
     return "wmma_tiled_tuned"
 
 
-def _scale_fmt(scales: torch.Tensor, weight_is_e2m1: bool, what: str) -> int:
+def _scale_fmt(scales: torch.Tensor, weight_is_e2m1: bool, what: str, has_zeros: bool = False) -> int:
+    """The scale policy from the scales dtype plus the zeros slot (python/minisgl/quant/kernels.py:
+    1137-1146, 518-559): fp16 -> folded group scales; uint8 without zeros -> MXFP4 E8M0; e4m3, or
+    uint8 with the zeros slot populated -> NVFP4 block scales with the per-channel f32 global."""
     if scales.dtype == torch.float16:
         return _abi.SCALE_F16
-    if scales.dtype == torch.uint8:
+    if scales.dtype in (torch.uint8, torch.float8_e4m3fn):
         if not weight_is_e2m1:
-            raise TypeError(f"{what}: uint8 (E8M0) scales are only valid for e2m1 weights")
+            raise TypeError(f"{what}: one-byte (E8M0 / e4m3) scales are only valid for e2m1 weights")
+        if scales.dtype == torch.float8_e4m3fn or has_zeros:
+            return _abi.SCALE_E4M3
         return _abi.SCALE_E8M0
-    raise TypeError(f"{what}: scales must be fp16 (group scales) or uint8 (E8M0), got {scales.dtype}")
+    raise TypeError(f"{what}: scales must be fp16 (group scales), uint8 (E8M0) or float8_e4m3fn/uint8 with the "
+                    f"NVFP4 global (e4m3 block scales), got {scales.dtype}")
+
+
+def _nvfp4_global(w_zeros: torch.Tensor | None, N: int, what: str) -> torch.Tensor:
+    """The NVFP4 per-output-channel f32 global multiplier, as the int32 bit pattern the zeros slot
+    carries. A `.to(torch.int32)` of the floats instead of a view would truncate them, so only f32
+    (viewed here) or an int32 bit pattern are accepted."""
+    if w_zeros is None or w_zeros.numel() == 0:
+        raise AssertionError(f"{what}: e4m3 block scales REQUIRE the per-output-channel f32 global in the "
+                             f"zeros slot; the two-level scale is incomplete without it")
+    if tuple(w_zeros.shape) != (N,) or w_zeros.dtype not in (torch.float32, torch.int32):
+        raise AssertionError(f"{what}: the NVFP4 global must be an (N,)=({N},) f32 vector (or its int32 bit "
+                             f"pattern), got {w_zeros.dtype} {tuple(w_zeros.shape)}")
+    return w_zeros.contiguous().view(torch.int32)
 
 
 def _check_producer_pair(x: torch.Tensor, x_fp8, act_scales, what: str):
@@ -230,7 +249,8 @@ def _check_producer_pair(x: torch.Tensor, x_fp8, act_scales, what: str):
 
 
 def _dense_prep(x, w_packed, scales, w_zeros, group_size, weight_is_e2m1, what):
-    """Shape/dtype checks shared by the dense arms; returns (M, K, N, sfmt, w_zeros, tiles)."""
+    """Shape/dtype checks shared by the dense arms; returns (M, K, N, sfmt, w_zeros, scales) with the
+    zeros slot and the scales in the form the C ABI takes."""
     if x.dim() != 2 or x.dtype not in (torch.bfloat16, torch.float16):
         raise TypeError(f"{what}: x must be 2-D bf16/fp16, got {x.dtype} {tuple(x.shape)}")
     M, K = x.shape
@@ -239,36 +259,25 @@ def _dense_prep(x, w_packed, scales, w_zeros, group_size, weight_is_e2m1, what):
     if K % group_size or tuple(scales.shape) != (G, N):
         raise AssertionError(f"{what}: scales must be GROUP-major (K//group, N)=({G}, {N}), got "
                              f"{tuple(scales.shape)}")
-    sfmt = _scale_fmt(scales, weight_is_e2m1, what)
-    if weight_is_e2m1 and w_zeros is not None and w_zeros.numel() > 0:
-        raise AssertionError(f"{what}: e2m1 weights are symmetric; w_zeros must be None")
-    if w_zeros is not None and w_zeros.numel() == 0:
-        w_zeros = None
-    if w_zeros is not None and (w_zeros.dtype != torch.int32 or tuple(w_zeros.shape) != (G, N // 8)):
-        raise AssertionError(f"{what}: w_zeros must be (K//group, N/8)=({G}, {N // 8}) int32, got "
-                             f"{w_zeros.dtype} {tuple(w_zeros.shape)}")
-    tiles = _as_tiles(w_packed, K, weight_is_e2m1, 2, what)
-    return M, K, N, sfmt, w_zeros, tiles
+    has_zeros = w_zeros is not None and w_zeros.numel() > 0
+    sfmt = _scale_fmt(scales, weight_is_e2m1, what, has_zeros)
+    if sfmt == _abi.SCALE_E4M3:
+        w_zeros = _nvfp4_global(w_zeros, N, what)
+        scales = scales.view(torch.uint8)
+    else:
+        if weight_is_e2m1 and has_zeros:
+            raise AssertionError(f"{what}: e2m1 weights are symmetric; w_zeros must be None")
+        if not has_zeros:
+            w_zeros = None
+        if w_zeros is not None and (w_zeros.dtype != torch.int32 or tuple(w_zeros.shape) != (G, N // 8)):
+            raise AssertionError(f"{what}: w_zeros must be (K//group, N/8)=({G}, {N // 8}) int32, got "
+                                 f"{w_zeros.dtype} {tuple(w_zeros.shape)}")
+    return M, K, N, sfmt, w_zeros, scales
 
 
 def _dense(x, w_packed, scales, w_zeros, group_size, weight_is_e2m1, x_fp8, act_scales, silu, arm):
     what = "w4a8_linear_silu" if silu else "w4a8_linear"
-    if x.dim() != 2 or x.dtype not in (torch.bfloat16, torch.float16):
-        raise TypeError(f"{what}: x must be 2-D bf16/fp16, got {x.dtype} {tuple(x.shape)}")
-    M, K = x.shape
-    N = _n_of(w_packed)
-    G = K // group_size
-    if K % group_size or tuple(scales.shape) != (G, N):
-        raise AssertionError(f"{what}: scales must be GROUP-major (K//group, N)=({G}, {N}), got "
-                             f"{tuple(scales.shape)}")
-    sfmt = _scale_fmt(scales, weight_is_e2m1, what)
-    if weight_is_e2m1 and w_zeros is not None and w_zeros.numel() > 0:
-        raise AssertionError(f"{what}: e2m1 weights are symmetric; w_zeros must be None")
-    if w_zeros is not None and w_zeros.numel() == 0:
-        w_zeros = None
-    if w_zeros is not None and (w_zeros.dtype != torch.int32 or tuple(w_zeros.shape) != (G, N // 8)):
-        raise AssertionError(f"{what}: w_zeros must be (K//group, N/8)=({G}, {N // 8}) int32, got "
-                             f"{w_zeros.dtype} {tuple(w_zeros.shape)}")
+    M, K, N, sfmt, w_zeros, scales = _dense_prep(x, w_packed, scales, w_zeros, group_size, weight_is_e2m1, what)
     xq, xs = _check_producer_pair(x, x_fp8, act_scales, what)
     tiles = _as_tiles(w_packed, K, weight_is_e2m1, 2, what)
     nout = N // 2 if silu else N
@@ -356,7 +365,8 @@ def w4a8_linear_silu(
 # MoE
 # --------------------------------------------------------------------------------------------
 def _w4a16(x, w_packed, scales, w_zeros, group_size, weight_is_e2m1, silu, what):
-    M, K, N, sfmt, w_zeros, tiles = _dense_prep(x, w_packed, scales, w_zeros, group_size, weight_is_e2m1, what)
+    M, K, N, sfmt, w_zeros, scales = _dense_prep(x, w_packed, scales, w_zeros, group_size, weight_is_e2m1, what)
+    tiles = _as_tiles(w_packed, K, weight_is_e2m1, 2, what)
     if K % 8:
         raise AssertionError(f"{what}: K={K} must be a multiple of 8")
     kernel = _pick_dense_kernel(M, weight_is_e2m1, group_size, k=K, n=N)

@@ -117,34 +117,42 @@ def act_quant(x_bits: np.ndarray, dtype: int = 0) -> tuple[np.ndarray, np.ndarra
     return q, s
 
 
+def _scales_arg(scales: np.ndarray, zeros, nvfp4: bool):
+    """(scale buffer, format code, zeros/global buffer). NVFP4: e4m3 block-scale bytes (uint8) with the
+    per-channel f32 global multiplier in the zeros slot (f32 or its int32 bit pattern)."""
+    if nvfp4:
+        sc, fmt = np.ascontiguousarray(scales, dtype=np.uint8), 2
+        z = np.ascontiguousarray(np.asarray(zeros).view(np.int32) if np.asarray(zeros).dtype == np.float32
+                                 else zeros, dtype=np.int32)
+        return sc, fmt, z
+    if scales.dtype == np.float16:
+        sc, fmt = np.ascontiguousarray(scales).view(np.uint16), 0
+    else:
+        sc, fmt = np.ascontiguousarray(scales, dtype=np.uint8), 1
+    return sc, fmt, None if zeros is None else np.ascontiguousarray(zeros, dtype=np.int32)
+
+
 def gemm(xq: np.ndarray, xs: np.ndarray, w_packed: np.ndarray, scales: np.ndarray, zeros: np.ndarray | None,
-         group: int, e2m1: bool = False) -> np.ndarray:
+         group: int, e2m1: bool = False, nvfp4: bool = False) -> np.ndarray:
     """f64 y[m,n] = s_m * sum_g scale[g,n] * sum_{k in g} e4m3(q[m,k]) * w(n,k).
-    scales: (G,N) float16 (passed as its uint16 bits) or uint8 E8M0."""
+    scales: (G,N) float16 (passed as its uint16 bits), uint8 E8M0, or (nvfp4) e4m3 bytes with the
+    (N,) f32 global in zeros."""
     xq = np.ascontiguousarray(xq, dtype=np.uint8)
     xs = np.ascontiguousarray(xs, dtype=np.float32)
     w = np.ascontiguousarray(w_packed, dtype=np.int32)
     M, K = xq.shape
     N = w.shape[0]
-    if scales.dtype == np.float16:
-        sc, fmt = np.ascontiguousarray(scales).view(np.uint16), 0
-    else:
-        sc, fmt = np.ascontiguousarray(scales, dtype=np.uint8), 1
-    z = None if zeros is None else np.ascontiguousarray(zeros, dtype=np.int32)
+    sc, fmt, z = _scales_arg(scales, zeros, nvfp4)
     out = np.empty((M, N), dtype=np.float64)
     lib().w4o_gemm(_p(xq), _p(xs), M, K, _p(w), N, _p(sc), fmt, _p(z), int(e2m1), group, _p(out))
     return out
 
 
 def dequant(w_packed: np.ndarray, scales: np.ndarray, zeros: np.ndarray | None, group: int,
-            e2m1: bool = False) -> np.ndarray:
+            e2m1: bool = False, nvfp4: bool = False) -> np.ndarray:
     w = np.ascontiguousarray(w_packed, dtype=np.int32)
     N, K = w.shape[0], w.shape[1] * 8
-    if scales.dtype == np.float16:
-        sc, fmt = np.ascontiguousarray(scales).view(np.uint16), 0
-    else:
-        sc, fmt = np.ascontiguousarray(scales, dtype=np.uint8), 1
-    z = None if zeros is None else np.ascontiguousarray(zeros, dtype=np.int32)
+    sc, fmt, z = _scales_arg(scales, zeros, nvfp4)
     out = np.empty((N, K), dtype=np.float64)
     lib().w4o_dequant(_p(w), N, K, _p(sc), fmt, _p(z), int(e2m1), group, _p(out))
     return out
@@ -225,7 +233,7 @@ def act_split(x_bits: np.ndarray, dtype: int = 0) -> tuple[np.ndarray, np.ndarra
 
 
 def w4a16_gemm(x_bits: np.ndarray, dtype: int, w_packed: np.ndarray, scales: np.ndarray, zeros: np.ndarray | None,
-               group: int, e2m1: bool = False) -> np.ndarray:
+               group: int, e2m1: bool = False, nvfp4: bool = False) -> np.ndarray:
     """f64 y = x @ dequant(W)^T with x decoded exactly from its bf16/fp16 bits (the unquantized
     activations of python/minisgl/quant/kernels.py:1125-1178)."""
     xb = np.ascontiguousarray(x_bits, dtype=np.uint16)
@@ -233,4 +241,4 @@ def w4a16_gemm(x_bits: np.ndarray, dtype: int, w_packed: np.ndarray, scales: np.
         x = bf16_to_f32(xb).astype(np.float64)
     else:
         x = xb.view(np.float16).astype(np.float64)
-    return x @ dequant(w_packed, scales, zeros, group, e2m1).T
+    return x @ dequant(w_packed, scales, zeros, group, e2m1, nvfp4).T

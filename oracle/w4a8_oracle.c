@@ -184,8 +184,16 @@ static inline double weight_val(const int32_t* w_packed, const int32_t* zeros, i
   return (double)(c - z);
 }
 
-static inline double scale_val(const void* scales, int scale_fmt, int64_t N, int64_t g, int64_t n) {
+/* scale_fmt 2 (NVFP4, python/minisgl/quant/nvfp4.py:1-60 and quant/kernels.py:518-559): an e4m3
+ * block scale times the per-output-channel f32 global multiplier, which rides the zeros slot. */
+static inline double scale_val(const void* scales, int scale_fmt, int64_t N, int64_t g, int64_t n,
+                               const int32_t* zeros) {
   if (scale_fmt == 1) return w4o_e8m0_to_f64(((const uint8_t*)scales)[g * N + n]);
+  if (scale_fmt == 2) {
+    float glob;
+    memcpy(&glob, &zeros[n], 4);
+    return (double)w4o_e4m3_to_f32(((const uint8_t*)scales)[g * N + n]) * (double)glob;
+  }
   return (double)w4o_f16_to_f32(((const uint16_t*)scales)[g * N + n]);
 }
 
@@ -209,7 +217,7 @@ void w4o_gemm(const uint8_t* xq, const float* act_scales, int64_t M, int64_t K,
 #pragma omp for schedule(static)
     for (int64_t n = 0; n < N; ++n) {
       for (int64_t k = 0; k < K; ++k) wrow[k] = weight_val(w_packed, zeros, N, K, group, e2m1, n, k);
-      for (int64_t g = 0; g < G; ++g) sc[g] = scale_val(scales, scale_fmt, N, g, n);
+      for (int64_t g = 0; g < G; ++g) sc[g] = scale_val(scales, scale_fmt, N, g, n, zeros);
       for (int64_t m = 0; m < M; ++m) {
         const double* xr = xv + m * K;
         double acc = 0.0;
@@ -233,7 +241,7 @@ void w4o_dequant(const int32_t* w_packed, int64_t N, int64_t K, const void* scal
                  const int32_t* zeros, int e2m1, int64_t group, double* out) {
   for (int64_t n = 0; n < N; ++n)
     for (int64_t k = 0; k < K; ++k)
-      out[n * K + k] = scale_val(scales, scale_fmt, N, k / group, n) *
+      out[n * K + k] = scale_val(scales, scale_fmt, N, k / group, n, zeros) *
                        weight_val(w_packed, zeros, N, K, group, e2m1, n, k);
 }
 

@@ -59,6 +59,19 @@ def mxfp4_weight(N: int, K: int, seed: int, E: int | None = None):
     return pack_rows(codes), scales
 
 
+def nvfp4_weight(N: int, K: int, seed: int, E: int | None = None):
+    """NVFP4 (python/minisgl/quant/nvfp4.py:1-60): e2m1 codes uniform over the 16 values; e4m3
+    block-16 scales as group-major (K/16, N) float8_e4m3fn, positive, |N(0,1)| * 8 + 0.5 (so they
+    span several binades and use the mantissa bits); a per-output-channel f32 global multiplier
+    |N(0, 1e-3)| + 1e-4 (the modelopt spelling, already direction-normalised)."""
+    g = gen(seed)
+    lead = () if E is None else (E,)
+    codes = torch.randint(0, 16, (*lead, N, K), generator=g, dtype=torch.int32)
+    scales = (torch.randn(*lead, K // 16, N, generator=g).abs() * 8 + 0.5).to(torch.float8_e4m3fn)
+    glob = torch.randn(*lead, N, generator=g).abs() * 1e-3 + 1e-4
+    return pack_rows(codes), scales, glob.to(torch.float32)
+
+
 def router_logits(T: int, E: int, seed: int, dtype=torch.bfloat16) -> torch.Tensor:
     return torch.randn(T, E, generator=gen(seed)).to(dtype)
 

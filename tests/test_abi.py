@@ -121,8 +121,14 @@ def test_scale_layout_and_format_refusals():
     with pytest.raises(TypeError, match="E8M0"):
         K_.w4a8_linear(x, w, torch.zeros((256 // 32, 64), dtype=torch.uint8), None, 32)
     with pytest.raises(AssertionError, match="symmetric"):
+        K_.w4a8_linear(x, w, torch.ones((8, 64), dtype=torch.float16), torch.zeros((8, 8), dtype=torch.int32), 32,
+                       weight_is_e2m1=True)
+    # one-byte scales with the zeros slot populated are NVFP4: the slot must hold the (N,) f32 global
+    with pytest.raises(AssertionError, match="NVFP4 global"):
         K_.w4a8_linear(x, w, torch.zeros((8, 64), dtype=torch.uint8), torch.zeros((8, 8), dtype=torch.int32), 32,
                        weight_is_e2m1=True)
+    with pytest.raises(AssertionError, match="REQUIRE"):
+        K_.w4a8_linear(x, w, torch.zeros((16, 64), dtype=torch.float8_e4m3fn), None, 16, weight_is_e2m1=True)
 
 
 # tests/mxfp4_moe_scale_guard_test.py:27-58 restated against this provider

@@ -414,3 +414,16 @@ def test_w4a16_gemm_reference_brute_force(oracle):
         for n in range(N):
             want[m, n] = sum(float(x[m, k]) * (codes[n, k] - zz[k // g, n]) * s64[k // g, n] for k in range(K))
     assert np.allclose(ref, want, rtol=1e-12, atol=1e-12)
+
+
+def test_nvfp4_dequant_is_two_level(oracle):
+    """NVFP4 dequant = e2m1 LUT value * e4m3 block scale (torch's decode) * per-channel global,
+    with group 16 (python/minisgl/quant/nvfp4.py:12-18)."""
+    N, K = 32, 64
+    w, s, glob = synth.nvfp4_weight(N, K, seed=5)
+    got = oracle.dequant(w.numpy(), s.view(torch.uint8).numpy(), glob.numpy(), 16, e2m1=True, nvfp4=True)
+    codes = ((w.numpy()[:, :, None] >> (4 * np.arange(8))) & 15).reshape(N, K)
+    lut = oracle.E2M1_LUT[codes]
+    sc = s.to(torch.float32).numpy().astype(np.float64)  # (K/16, N)
+    want = lut * sc.T.repeat(16, axis=1) * glob.numpy().astype(np.float64)[:, None]
+    assert np.array_equal(got, want)
