@@ -558,8 +558,8 @@ def _check_moe_scale_pair(w: torch.Tensor, scales: torch.Tensor, zeros: "torch.T
     """The (scales dtype, zeros slot) pair must be one the grouped kernel dispatches
     (python/minisgl/quant/kernels.py:484-559): fp16 folded scales with optional (E, G, N/8) AWQ
     zeros; uint8 without zeros is MXFP4 E8M0. The NVFP4 two-level form (e4m3/uint8 block scale
-    with an (E, N) f32-as-int32 global) is recognised and validated exactly as there, and then
-    refused by w4a8_moe as outside this build."""
+    with an (E, N) f32-as-int32 global) is validated exactly as there and served by the e2m1
+    kernels with 16-wide groups."""
     if scales.dtype == torch.float16:
         if zeros is not None and zeros.dim() != 3:
             raise AssertionError(
@@ -646,10 +646,6 @@ def _moe_forward(x, w13, w13_scales, w13_zeros, w2, w2_scales, w2_zeros, gating_
     )
     _check_moe_scale_pair(w13, w13_scales, w13_zeros, "w13")
     _check_moe_scale_pair(w2, w2_scales, w2_zeros, "w2")
-    for s, z in ((w13_scales, w13_zeros), (w2_scales, w2_zeros)):
-        if s.dtype == torch.float8_e4m3fn or (s.dtype == torch.uint8 and z is not None):
-            raise NotImplementedError("w4a8_moe: NVFP4 two-level scales are outside this build (W4A8 int4 and "
-                                      "MXFP4 E8M0 only)")
     assert activation in ("silu", "gelu"), (
         f"w4a8_moe supports activation 'silu' or 'gelu' (gelu_pytorch_tanh); got {activation!r}")
     if activation != "silu":
@@ -694,8 +690,12 @@ def _moe_forward(x, w13, w13_scales, w13_zeros, w2, w2_scales, w2_zeros, gating_
     wfmt = _abi.W_E2M1 if weight_is_e2m1 else _abi.W_INT4
     t13 = _as_tiles(w13, K, weight_is_e2m1, 3, "w4a8_moe w13")
     t2 = _as_tiles(w2, inter, weight_is_e2m1, 3, "w4a8_moe w2")
-    s13f = _scale_fmt(w13_scales, weight_is_e2m1, "w4a8_moe w13")
-    s2f = _scale_fmt(w2_scales, weight_is_e2m1, "w4a8_moe w2")
+    s13f = _scale_fmt(w13_scales, weight_is_e2m1, "w4a8_moe w13", w13_zeros is not None)
+    s2f = _scale_fmt(w2_scales, weight_is_e2m1, "w4a8_moe w2", w2_zeros is not None)
+    if s13f == _abi.SCALE_E4M3:
+        w13_scales = w13_scales.view(torch.uint8)
+    if s2f == _abi.SCALE_E4M3:
+        w2_scales = w2_scales.view(torch.uint8)
     arm = _abi.KERNEL_DECODE if block_m < 64 else _abi.KERNEL_PREFILL
     arm_name = "gemv" if arm == _abi.KERNEL_DECODE else "mfma"
     e2 = "+e2m1" if weight_is_e2m1 else ""

@@ -181,20 +181,23 @@ def moe_align(ids: np.ndarray, E: int, bm: int):
 
 
 def moe_forward(x_bits, dtype, tw, sorted_ids, expert_ids, ntp, bm, top_k, w13, s13, z13, w2, s2, z2,
-                e2m1=False, with_buf2=False):
-    """Full grouped W4A8 MoE forward in f64 -> (T, H) (before the dtype cast)."""
+                e2m1=False, with_buf2=False, nvfp4=False):
+    """Full grouped W4A8 MoE forward in f64 -> (T, H) (before the dtype cast). nvfp4: e4m3 block-scale
+    bytes in s13/s2 and the (E, N) f32 globals in z13/z2."""
     x = np.ascontiguousarray(x_bits, dtype=np.uint16)
     T, H = x.shape
     E, N1 = w13.shape[0], w13.shape[1]
     I = N1 // 2
     g1 = H // s13.shape[1]
     g2 = I // s2.shape[1]
-    fmt = 0 if s13.dtype == np.float16 else 1
+    fmt = 2 if nvfp4 else 0 if s13.dtype == np.float16 else 1
     conv = (lambda a: np.ascontiguousarray(a).view(np.uint16)) if fmt == 0 else (lambda a: np.ascontiguousarray(a, dtype=np.uint8))
     a13, a2 = conv(s13), conv(s2)
     w13c, w2c = np.ascontiguousarray(w13, dtype=np.int32), np.ascontiguousarray(w2, dtype=np.int32)
-    z13c = None if z13 is None else np.ascontiguousarray(z13, dtype=np.int32)
-    z2c = None if z2 is None else np.ascontiguousarray(z2, dtype=np.int32)
+    zc = (lambda z: np.ascontiguousarray(np.asarray(z, dtype=np.float32)).view(np.int32)) if nvfp4 else \
+        (lambda z: np.ascontiguousarray(z, dtype=np.int32))
+    z13c = None if z13 is None else zc(z13)
+    z2c = None if z2 is None else zc(z2)
     out = np.empty((T, H), dtype=np.float64)
     buf2 = np.zeros((max(ntp, 1), I), dtype=np.uint16) if with_buf2 else None
     twc = np.ascontiguousarray(tw, dtype=np.float32)

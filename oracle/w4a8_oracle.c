@@ -366,7 +366,9 @@ void w4o_moe_forward(const uint16_t* x, int dtype, int64_t T, int64_t H, int64_t
   double* y2 = (double*)malloc(sizeof(double) * (size_t)H);
   int64_t sz13 = N1 * (H / 8), szs13 = (H / g1) * N1, szz13 = (H / g1) * (N1 / 8);
   int64_t sz2 = H * (I / 8), szs2 = (I / g2) * H, szz2 = (I / g2) * (H / 8);
-  int sb = scale_fmt == 1 ? 1 : 2;
+  /* NVFP4: the zeros slot is the (E, N) f32 global (python/minisgl/quant/kernels.py:547-559) */
+  if (scale_fmt == 2) { szz13 = N1; szz2 = H; }
+  int sb = scale_fmt == 0 ? 2 : 1;
   memset(out, 0, sizeof(double) * (size_t)(T * H));
   for (int64_t p = 0; p < ntp; ++p) {
     int32_t r = sorted_ids[p];
