@@ -145,6 +145,42 @@ class _GroupedMxFp4Experts:
         del self.weight_packed, self.weight_scale
 
 
+class _GroupedNvFp4Experts:
+    """NVFP4 experts (python/minisgl/layers/moe.py:346-407): weight_packed (E, N, K/2) uint8,
+    weight_scale (E, N, K/16) float8_e4m3fn block scales (byte-verbatim), weight_global (E, N) f32
+    per-output-channel multipliers (direction-normalised by the loader). After post_load: _w_op W4
+    tiles, _scales_op (E, K/16, N) e4m3 group-major, _zeros_op the (E, N) globals' f32 bits as int32
+    (the zeros slot of the grouped kernels)."""
+
+    def __init__(self, num_experts: int, out_features: int, in_features: int, quant):
+        N, K = out_features, in_features
+        assert quant.group_size == 16, f"NVFP4 blocks are 16 elements; got group_size={quant.group_size}"
+        assert K % 32 == 0 and N % 16 == 0, f"grouped NVFP4 needs K%32==0,N%16==0; got N={N},K={K}"
+        self.weight_packed = torch.empty((num_experts, N, K // 2), dtype=torch.uint8)
+        self.weight_scale = torch.empty((num_experts, N, K // 16), dtype=torch.float8_e4m3fn)
+        self.weight_global = torch.empty((num_experts, N), dtype=torch.float32)
+        self._quant = quant
+        self._num_experts = num_experts
+
+    def forward(self, *args, **kwargs):
+        raise RuntimeError(f"{type(self).__name__} holds weights; call kernels.w4a8_moe instead")
+
+    def post_load(self) -> None:
+        nvfp4 = importlib.import_module(f"{_pkg}.quant.nvfp4")
+        conv = nvfp4.convert_nvfp4_moe(self.weight_packed, self.weight_scale)
+        self._w_op = _finish(conv["w_packed"], True)
+        self._scales_op = conv["scales"].transpose(1, 2).contiguous()  # (E, K/16, N)
+        # a view, never .to(int32): the value conversion would truncate every global to 0
+        self._zeros_op = self.weight_global.to(torch.float32).contiguous().view(torch.int32)
+        del self.weight_packed, self.weight_scale, self.weight_global
+
+
+def _no_moe_w4a16(scheme: str) -> None:
+    if kernels.MOE_W4A16 != "0":
+        raise NotImplementedError(f"MoE {scheme}: the W4A16 expert arm (MINISGL_MOE_W4A16) is not built for MI355X; "
+                                  f"unset MINISGL_MOE_W4A16 to serve the experts through the W4A8 path")
+
+
 class MoEQuantMethod:
     """How a MoE expert pair (w13 gate|up, w2 down) allocates its weights and runs its grouped GEMMs
     (python/minisgl/layers/moe.py:520-580)."""
@@ -203,6 +239,7 @@ class _W4A8MoEMethod(MoEQuantMethod):
     def apply(self, w13, w2, hidden_states, *, router_logits, topk_weights, topk_ids, top_k, renormalize,
               activation, apply_router_weight_on_input, x_fp8=None, act_scales=None):
         _check_activation("W4A8", activation)
+        _no_moe_w4a16("W4A8")
         assert not apply_router_weight_on_input, "MoE W4A8 path has no router-weight-on-input"
         return kernels.w4a8_moe(hidden_states, w13._w_op, w13._scales_op, w13._zeros_op,
                                 w2._w_op, w2._scales_op, w2._zeros_op, router_logits, top_k, renormalize,
@@ -232,6 +269,7 @@ class _MxFp4MoEMethod(MoEQuantMethod):
     def apply(self, w13, w2, hidden_states, *, router_logits, topk_weights, topk_ids, top_k, renormalize,
               activation, apply_router_weight_on_input, x_fp8=None, act_scales=None):
         _check_activation("MXFP4", activation)
+        _no_moe_w4a16("MXFP4")
         assert not apply_router_weight_on_input, "MoE MXFP4 path has no router-weight-on-input"
         return kernels.w4a8_moe(hidden_states, w13._w_op, w13._scales_op, None, w2._w_op, w2._scales_op, None,
                                 router_logits, top_k, renormalize, topk_weights=topk_weights, topk_ids=topk_ids,
@@ -244,16 +282,48 @@ class _MxFp4MoEMethod(MoEQuantMethod):
                                 weight_is_e2m1=True, activation=activation)
 
 
+class _NvFp4MoEMethod(MoEQuantMethod):
+    """NVFP4 grouped experts through kernels.w4a8_moe: e2m1 codes, e4m3 block-16 scales and the
+    (E, N) globals in the zeros slot (python/minisgl/layers/moe.py:785-883)."""
+
+    supports_ep = True
+    supports_producer_actquant = True
+    cache_plane_attrs = ("_w_op", "_scales_op", "_zeros_op")
+
+    def __init__(self, quant):
+        self._quant = quant
+
+    def create_experts(self, num_experts, out_features, in_features):
+        return _GroupedNvFp4Experts(num_experts, out_features, in_features, self._quant)
+
+    def apply(self, w13, w2, hidden_states, *, router_logits, topk_weights, topk_ids, top_k, renormalize,
+              activation, apply_router_weight_on_input, x_fp8=None, act_scales=None):
+        _check_activation("NVFP4", activation)
+        _no_moe_w4a16("NVFP4")
+        assert not apply_router_weight_on_input, "MoE NVFP4 path has no router-weight-on-input"
+        return kernels.w4a8_moe(hidden_states, w13._w_op, w13._scales_op, w13._zeros_op, w2._w_op, w2._scales_op,
+                                w2._zeros_op, router_logits, top_k, renormalize, topk_weights=topk_weights,
+                                topk_ids=topk_ids, weight_is_e2m1=True, activation=activation, x_fp8=x_fp8,
+                                act_scales=act_scales)
+
+    def ep_local(self, w13, w2, g_hidden, local_weights, local_ids, *, top_k, renormalize, activation="silu"):
+        _check_activation("NVFP4", activation)
+        _no_moe_w4a16("NVFP4")
+        return kernels.w4a8_moe(g_hidden, w13._w_op, w13._scales_op, w13._zeros_op, w2._w_op, w2._scales_op,
+                                w2._zeros_op, None, top_k, renormalize, topk_weights=local_weights,
+                                topk_ids=local_ids, weight_is_e2m1=True, activation=activation)
+
+
 def create_moe_quant_method(quant, *, fp8_experts: bool = False) -> MoEQuantMethod:
     """Pick the expert method from the declared scheme (python/minisgl/layers/moe.py:971-1005):
-    MXFP4 -> _MxFp4MoEMethod, int4 AWQ/GPTQ/compressed-tensors -> _W4A8MoEMethod. Unquantized,
-    fp8 and NVFP4 experts are other paths and raise NotImplementedError here."""
+    NVFP4 -> _NvFp4MoEMethod, MXFP4 -> _MxFp4MoEMethod, int4 AWQ/GPTQ/compressed-tensors ->
+    _W4A8MoEMethod. Unquantized and fp8 experts are other paths and raise NotImplementedError here."""
     if fp8_experts or (quant is not None and quant.is_fp8_w8a8):
         raise NotImplementedError("fp8 W8A8 experts are not served by this W4A8 path")
     if quant is None:
         raise NotImplementedError("unquantized experts are not served by this W4A8 path")
     if quant.is_nvfp4:
-        raise NotImplementedError("NVFP4 experts are not served by this W4A8 path")
+        return _NvFp4MoEMethod(quant)
     if quant.weight_is_e2m1:
         return _MxFp4MoEMethod(quant)
     if quant.is_int4:

@@ -32,6 +32,10 @@ _W4A8_GEMV_MAX_INT4 = 16
 _W4A8_GEMV_MAX_E2M1 = 16
 _W4A8_GEMV_K_MULTIPLE = 32
 
+# The W4A16 arm (unquantized activations) of the linear methods is opt-in, read once at import
+# (python/minisgl/quant/kernels.py MOE_W4A16 / MINISGL_MOE_W4A16).
+MOE_W4A16 = os.environ.get("MINISGL_MOE_W4A16", "0")
+
 # MoE gemm1 GEMV crossover and tile heights (python/minisgl/quant/kernels.py:130-131, 349-353).
 _MOE_GEMM1_GEMV_MAX = 32
 _MOE_WMMA_DIM = 16

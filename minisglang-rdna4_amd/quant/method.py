@@ -3,6 +3,7 @@ converts them once after load, and runs its GEMM.
 
 Mirrors the reference's method protocol and its W4A8 members (python/minisgl/quant/method.py):
 LinearMethod (:352-364), W4A8LinearMethod (:384-574), MxFp4LinearMethod (:577-677),
+NvFp4LinearMethod (:708-790),
 create_linear_method (:680-705), the fused-SwiGLU shape gate _fused_swiglu_ok (:29-58) and the
 compressed-tensors packed-sign decision (ct_packed_sign_convention / apply_ct_sign, :99-250).
 
@@ -12,8 +13,9 @@ Differences by design:
     on a CPU-resident layer it stops at the op layout (the kernels accept both).
   * GPTQ's explicitly stored symmetric zero points (all 8) collapse to None: the kernels' symmetric
     path computes exactly the same values without reading a zero-point tensor.
-  * The W4A16 arms and the NVFP4 / fp8 methods are outside this package: create_linear_method
-    raises NotImplementedError for those schemes rather than routing them elsewhere.
+  * The W4A16 arm (MINISGL_MOE_W4A16 != "0") runs the same weights through kernels.w4a16_linear;
+    NVFP4 keeps its two-level scale (NvFp4LinearMethod). The fp8 methods are outside this package:
+    create_linear_method raises NotImplementedError for those schemes.
 """
 from __future__ import annotations
 
@@ -29,21 +31,28 @@ from .config import QuantConfig
 # ------------------------------------------------------------------------------------------------
 # fused SwiGLU gate
 # ------------------------------------------------------------------------------------------------
-def _group_supported(group_size: int, k: int) -> bool:
+def _group_supported(group_size: int, k: int, weight_is_e2m1: bool = False) -> bool:
     g = int(group_size)
-    ok = g in (32, 64) or (g >= 128 and (g & (g - 1)) == 0)
+    ok = g in (32, 64) or (g >= 128 and (g & (g - 1)) == 0) or (g == 16 and weight_is_e2m1)
     return ok and k % g == 0
 
 
-def _fused_swiglu_ok(x: torch.Tensor, w_packed: torch.Tensor, group_size: int) -> bool:
+def _fused_swiglu_ok(x: torch.Tensor, w_packed: torch.Tensor, group_size: int, weight_is_e2m1: bool = False) -> bool:
     """Shape gate for the fused gate_up + silu decode GEMV (python/minisgl/quant/method.py:29-58):
     exactly the kernel's own constraints, no stricter -- decode rows (M <= 16), K % 32 == 0, a group
-    size the kernel takes (32, 64 or a power of two >= 128 dividing K), and N = 2 * inter with
-    inter % 16 == 0 (whole 16-channel strips per half)."""
+    size the kernel takes (32, 64 or a power of two >= 128 dividing K; 16, NVFP4's block, for e2m1
+    weights), and N = 2 * inter with inter % 16 == 0 (whole 16-channel strips per half). No
+    scale-format restriction: fp16, E8M0 and NVFP4 scales all reach the fused arm."""
     n = kernels._n_of(w_packed)
     k = x.shape[-1]
     return (x.dim() == 2 and x.shape[0] <= 16 and k % 32 == 0 and n % 32 == 0
-            and _group_supported(group_size, k))
+            and _group_supported(group_size, k, weight_is_e2m1))
+
+
+def _w4a16() -> bool:
+    """The W4A16 arm (unquantized activations) is opt-in, as in the reference:
+    MINISGL_MOE_W4A16 != "0" (python/minisgl/quant/kernels.py MOE_W4A16)."""
+    return kernels.MOE_W4A16 != "0"
 
 
 # ------------------------------------------------------------------------------------------------
@@ -165,10 +174,13 @@ class W4A8LinearMethod:
       compressed-tensors int4: weight_packed (N, K/8) i32, weight_scale (N, K/g) f16,
             weight_zero_point (N/8, K/g) i32 when asymmetric."""
 
-    supports_producer_actquant = True
-
     def __init__(self, quant: QuantConfig) -> None:
         self.quant = quant
+
+    @property
+    def supports_producer_actquant(self) -> bool:
+        # the W4A16 arm reads x unquantized: a producer fp8 pair has nothing to feed
+        return not _w4a16()
 
     def create_weights(self, layer, out_features: int, in_features: int) -> None:
         pf = 32 // self.quant.bits
@@ -228,8 +240,12 @@ class W4A8LinearMethod:
 
     def apply(self, layer, x: torch.Tensor, bias: torch.Tensor | None, *,
               x_fp8: torch.Tensor | None = None, act_scales: torch.Tensor | None = None) -> torch.Tensor:
-        out = kernels.w4a8_linear(x, layer._w_packed_op, layer._scales_op, layer._zeros_op, self.quant.group_size,
-                                  x_fp8=x_fp8, act_scales=act_scales)
+        if _w4a16():
+            out = kernels.w4a16_linear(x, layer._w_packed_op, layer._scales_op, layer._zeros_op, self.quant.group_size,
+                                       kernels._n_of(layer._w_packed_op))
+        else:
+            out = kernels.w4a8_linear(x, layer._w_packed_op, layer._scales_op, layer._zeros_op, self.quant.group_size,
+                                      x_fp8=x_fp8, act_scales=act_scales)
         out = out.to(x.dtype)
         if bias is not None:
             out = out + bias
@@ -241,7 +257,8 @@ class W4A8LinearMethod:
         w = layer._w_packed_op
         if not _fused_swiglu_ok(x, w, self.quant.group_size):
             return None
-        return kernels.w4a8_linear_silu(x, w, layer._scales_op, layer._zeros_op, self.quant.group_size).to(x.dtype)
+        fn = kernels.w4a16_linear_silu if _w4a16() else kernels.w4a8_linear_silu
+        return fn(x, w, layer._scales_op, layer._zeros_op, self.quant.group_size).to(x.dtype)
 
 
 class MxFp4LinearMethod:
@@ -250,10 +267,12 @@ class MxFp4LinearMethod:
     weight_packed (N, K/2) uint8 (two E2M1 nibbles per byte, low nibble = lower K), weight_scale
     (N, K/32) uint8 E8M0. The E8M0 bytes reach the MFMA unchanged."""
 
-    supports_producer_actquant = True
-
     def __init__(self, quant: QuantConfig) -> None:
         self.quant = quant
+
+    @property
+    def supports_producer_actquant(self) -> bool:
+        return not _w4a16()
 
     def create_weights(self, layer, out_features: int, in_features: int) -> None:
         N, K = out_features, in_features
@@ -273,8 +292,12 @@ class MxFp4LinearMethod:
 
     def apply(self, layer, x: torch.Tensor, bias: torch.Tensor | None, *,
               x_fp8: torch.Tensor | None = None, act_scales: torch.Tensor | None = None) -> torch.Tensor:
-        out = kernels.w4a8_linear(x, layer._w_packed_op, layer._scales_op, None, self.quant.group_size,
-                                  weight_is_e2m1=True, x_fp8=x_fp8, act_scales=act_scales)
+        if _w4a16():
+            out = kernels.w4a16_linear(x, layer._w_packed_op, layer._scales_op, None, self.quant.group_size,
+                                       kernels._n_of(layer._w_packed_op), weight_is_e2m1=True)
+        else:
+            out = kernels.w4a8_linear(x, layer._w_packed_op, layer._scales_op, None, self.quant.group_size,
+                                      weight_is_e2m1=True, x_fp8=x_fp8, act_scales=act_scales)
         out = out.to(x.dtype)
         if bias is not None:
             out = out + bias
@@ -282,10 +305,65 @@ class MxFp4LinearMethod:
 
     def apply_swiglu(self, layer, x: torch.Tensor) -> torch.Tensor | None:
         w = getattr(layer, "_w_packed_op", None)
-        if w is None or not _fused_swiglu_ok(x, w, self.quant.group_size):
+        if w is None or not _fused_swiglu_ok(x, w, self.quant.group_size, weight_is_e2m1=True):
             return None
-        return kernels.w4a8_linear_silu(x, w, layer._scales_op, None, self.quant.group_size,
-                                        weight_is_e2m1=True).to(x.dtype)
+        fn = kernels.w4a16_linear_silu if _w4a16() else kernels.w4a8_linear_silu
+        return fn(x, w, layer._scales_op, None, self.quant.group_size, weight_is_e2m1=True).to(x.dtype)
+
+
+class NvFp4LinearMethod:
+    """NVFP4 dense linear (python/minisgl/quant/method.py:708-790): the e2m1 kernels with the
+    two-level scale kept as two levels. Checkpoint-native buffers: weight_packed (N, K/2) uint8 (two
+    E2M1 nibbles per byte, low nibble = lower K), weight_scale (N, K/16) float8_e4m3fn block scales
+    (byte-verbatim), weight_global (N,) f32 per-output-channel multiplier (the loader's
+    nvfp4.split_nvfp4_scale output, direction already normalised). After load: W4 tiles, group-major
+    (K/16, N) e4m3 scales and the global's f32 bits as int32 for the zeros slot."""
+
+    def __init__(self, quant: QuantConfig) -> None:
+        self.quant = quant
+
+    @property
+    def supports_producer_actquant(self) -> bool:
+        return not _w4a16()
+
+    def create_weights(self, layer, out_features: int, in_features: int) -> None:
+        N, K = out_features, in_features
+        g = self.quant.group_size
+        assert g == 16, f"NVFP4 blocks are 16 elements; got group_size={g}"
+        assert K % 32 == 0 and N % 16 == 0, f"NVFP4 needs K%32==0,N%16==0; got N={N},K={K}"
+        layer.weight_packed = torch.empty((N, K // 2), dtype=torch.uint8)
+        layer.weight_scale = torch.empty((N, K // g), dtype=torch.float8_e4m3fn)
+        layer.weight_global = torch.empty((N,), dtype=torch.float32)
+
+    def process_weights_after_load(self, layer) -> None:
+        from . import nvfp4
+
+        conv = nvfp4.convert_nvfp4_weight(layer.weight_packed, layer.weight_scale)
+        layer._w_packed_op = _to_kernel_layout(conv["w_packed"], True)
+        layer._scales_op = conv["scales"].transpose(0, 1).contiguous()  # (K/16, N) e4m3, group-major
+        # the f32 bits viewed as int32 (a value conversion would truncate every global to 0)
+        layer._global_op = layer.weight_global.to(torch.float32).contiguous().view(torch.int32)
+        del layer.weight_packed, layer.weight_scale, layer.weight_global
+
+    def apply(self, layer, x: torch.Tensor, bias: torch.Tensor | None, *,
+              x_fp8: torch.Tensor | None = None, act_scales: torch.Tensor | None = None) -> torch.Tensor:
+        if _w4a16():
+            out = kernels.w4a16_linear(x, layer._w_packed_op, layer._scales_op, layer._global_op, 16,
+                                       kernels._n_of(layer._w_packed_op), weight_is_e2m1=True)
+        else:
+            out = kernels.w4a8_linear(x, layer._w_packed_op, layer._scales_op, layer._global_op, 16,
+                                      weight_is_e2m1=True, x_fp8=x_fp8, act_scales=act_scales)
+        out = out.to(x.dtype)
+        if bias is not None:
+            out = out + bias
+        return out
+
+    def apply_swiglu(self, layer, x: torch.Tensor) -> torch.Tensor | None:
+        w = getattr(layer, "_w_packed_op", None)
+        if w is None or not _fused_swiglu_ok(x, w, 16, weight_is_e2m1=True):
+            return None
+        fn = kernels.w4a16_linear_silu if _w4a16() else kernels.w4a8_linear_silu
+        return fn(x, w, layer._scales_op, layer._global_op, 16, weight_is_e2m1=True).to(x.dtype)
 
 
 def create_linear_method(quant: QuantConfig | None, *, quantized: bool = True):
@@ -294,7 +372,7 @@ def create_linear_method(quant: QuantConfig | None, *, quantized: bool = True):
     if quant is None or not quantized:
         return UnquantizedLinearMethod()
     if quant.is_nvfp4:
-        raise NotImplementedError("NVFP4 (two-level e4m3 block + f32 global scale) is not served by this W4A8 path")
+        return NvFp4LinearMethod(quant)
     if quant.weight_is_e2m1:
         return MxFp4LinearMethod(quant)
     if quant.is_fp8_block or quant.is_fp8_w8a8:

@@ -139,3 +139,80 @@ def test_moe_method_matches_operator(kernels, dev):
     out_ep = m.ep_local(w13, w2, x, tw, ti, top_k=k, renormalize=True)
     torch.cuda.synchronize()
     assert torch.equal(out_ep, out)
+
+
+NV = C_.QuantConfig(method="compressed-tensors", bits=4, group_size=16, sym=True, weight_type="float",
+                    ct_format="nvfp4-pack-quantized")
+
+
+def _nv_layer(N, K, seed, dev):
+    g = synth.gen(seed)
+    codes = torch.randint(0, 16, (N, K), generator=g, dtype=torch.int32)
+    m = M_.create_linear_method(NV)
+    lay = SimpleNamespace()
+    m.create_weights(lay, N, K)
+    lay.weight_packed = (codes[:, 0::2] | (codes[:, 1::2] << 4)).to(torch.uint8).to(dev)
+    ws = (torch.rand(N, K // 16, generator=g) * 6 + 0.25).to(torch.float8_e4m3fn)
+    glob = torch.rand(N, generator=g) * 1e-3 + 1e-4
+    lay.weight_scale, lay.weight_global = ws.to(dev), glob.to(dev)
+    m.process_weights_after_load(lay)
+    return m, lay, codes, ws, glob
+
+
+def test_nvfp4_linear_method(kernels, oracle, dev):
+    """NVFP4 checkpoint buffers -> post_load -> apply, against the oracle's two-level dequant."""
+    N, K = 256, 1024
+    m, lay, codes, ws, glob = _nv_layer(N, K, 81, dev)
+    for M in (1, 3, 40):
+        x = synth.activations(M, K, seed=M).to(dev)
+        out = m.apply(lay, x, None)
+        torch.cuda.synchronize()
+        xq, xs = oracle.act_quant(synth.bits16(x.cpu()), 0)
+        ref = oracle.gemm(xq, xs, synth.pack_rows(codes).numpy(), ws.t().contiguous().view(torch.uint8).numpy(),
+                          glob.numpy(), 16, e2m1=True, nvfp4=True)
+        assert_close_to_oracle(out, ref, f"NVFP4 method M={M}")
+
+
+def test_w4a16_opt_in_routes_methods(kernels, dev, monkeypatch):
+    """MINISGL_MOE_W4A16 != "0": the dense methods run the W4A16 arm (no producer pair advertised),
+    bit-identical to w4a16_linear on the same tiles; MoE methods refuse it loudly."""
+    eng = pkg("_hip_engage")
+    N, K = 256, 512
+    m, lay, *_ = _nv_layer(N, K, 83, dev)
+    x = synth.activations(4, K, seed=4).to(dev)
+    monkeypatch.setattr(kernels, "MOE_W4A16", "1")
+    assert not m.supports_producer_actquant
+    before = eng.counts()
+    out = m.apply(lay, x, None)
+    ref = kernels.w4a16_linear(x, lay._w_packed_op, lay._scales_op, lay._global_op, 16, N, weight_is_e2m1=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    assert eng.counts_delta(before).get("w4a8_mi355x.w4a16_gemv+e2m1", 0) >= 1
+    mm = L_.create_moe_quant_method(GPTQ)
+    with pytest.raises(NotImplementedError, match="W4A16"):
+        mm.apply(None, None, x, router_logits=None, topk_weights=None, topk_ids=None, top_k=2, renormalize=True,
+                 activation="silu", apply_router_weight_on_input=False)
+
+
+def test_nvfp4_moe_method_matches_operator(kernels, dev):
+    E, H, I, T, k = 8, 256, 128, 5, 2
+    g = synth.gen(91)
+    m = L_.create_moe_quant_method(NV)
+    w13, w2 = m.create_experts(E, 2 * I, H), m.create_experts(E, H, I)
+    ops = []
+    for c, (n, kk) in ((w13, (2 * I, H)), (w2, (H, I))):
+        codes = torch.randint(0, 16, (E, n, kk), generator=g, dtype=torch.int32)
+        c.weight_packed = (codes[..., 0::2] | (codes[..., 1::2] << 4)).to(torch.uint8).to(dev)
+        c.weight_scale = (torch.rand(E, n, kk // 16, generator=g) * 6 + 0.25).to(torch.float8_e4m3fn).to(dev)
+        c.weight_global = (torch.rand(E, n, generator=g) * 1e-2 + 1e-3).to(dev)
+        ops.append((synth.pack_rows(codes).to(dev), c.weight_scale.transpose(1, 2).contiguous(),
+                    c.weight_global.view(torch.int32).clone()))
+        c.post_load()
+    x = synth.activations(T, H, seed=8).to(dev)
+    logits = synth.router_logits(T, E, seed=9).to(dev)
+    out = m.apply(w13, w2, x, router_logits=logits, topk_weights=None, topk_ids=None, top_k=k, renormalize=True,
+                  activation="silu", apply_router_weight_on_input=False)
+    ref = kernels.w4a8_moe(x, ops[0][0], ops[0][1], ops[0][2], ops[1][0], ops[1][1], ops[1][2], logits, k, True,
+                           weight_is_e2m1=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)

@@ -168,7 +168,8 @@ def test_fused_swiglu_gate_matches_kernel_constraints():
     assert M_._fused_swiglu_ok(x, w, 128)
     assert M_._fused_swiglu_ok(x, w, 32) and M_._fused_swiglu_ok(x, w, 64)
     assert not M_._fused_swiglu_ok(torch.zeros(17, 512, dtype=torch.bfloat16), w, 128)  # prefill
-    assert not M_._fused_swiglu_ok(x, w, 16)  # NVFP4 grouping is another path
+    assert not M_._fused_swiglu_ok(x, w, 16)  # 16-wide groups are e2m1-only
+    assert M_._fused_swiglu_ok(x, w, 16, weight_is_e2m1=True)  # NVFP4's block
     assert not M_._fused_swiglu_ok(x, torch.zeros(48, 64, dtype=torch.int32), 128)  # inter 24: not whole strips
     assert not M_._fused_swiglu_ok(torch.zeros(4, 500, dtype=torch.bfloat16), torch.zeros(256, 62, dtype=torch.int32), 128)
     tiles = torch.zeros(256 // 16, 4, 1024, dtype=torch.uint8)  # W4 tiles of the same weight
@@ -182,8 +183,7 @@ def test_create_linear_method_routes_by_declared_scheme():
     assert isinstance(M_.create_linear_method(MX), M_.MxFp4LinearMethod)
     assert isinstance(M_.create_linear_method(None), M_.UnquantizedLinearMethod)
     assert isinstance(M_.create_linear_method(AWQ, quantized=False), M_.UnquantizedLinearMethod)
-    with pytest.raises(NotImplementedError, match="NVFP4"):
-        M_.create_linear_method(NV)
+    assert isinstance(M_.create_linear_method(NV), M_.NvFp4LinearMethod)
     with pytest.raises(NotImplementedError, match="fp8"):
         M_.create_linear_method(FP8)
     assert M_.W4A8LinearMethod(AWQ).supports_producer_actquant
@@ -197,7 +197,9 @@ def test_moe_method_selection_and_containers():
     assert isinstance(L_.create_moe_quant_method(CT).create_experts(4, 64, 256), L_._GroupedCompressedTensorsExperts)
     mx = L_.create_moe_quant_method(MX)
     assert isinstance(mx, L_._MxFp4MoEMethod)
-    for q in (None, NV, FP8):
+    assert isinstance(L_.create_moe_quant_method(NV), L_._NvFp4MoEMethod)
+    assert isinstance(L_.create_moe_quant_method(NV).create_experts(4, 64, 256), L_._GroupedNvFp4Experts)
+    for q in (None, FP8):
         with pytest.raises(NotImplementedError):
             L_.create_moe_quant_method(q)
     with pytest.raises(NotImplementedError, match="activation"):
@@ -222,3 +224,58 @@ def test_moe_containers_post_load_per_expert():
     assert mx.weight_packed.shape == (E, N, K // 2) and mx.weight_scale.shape == (E, N, K // 32)
     mx.post_load()
     assert mx._w_op.shape == (E, N, K // 8) and mx._scales_op.shape == (E, K // 32, N)
+
+
+# ---------------------------------------------------------------------------------- NVFP4 loaders
+NV4 = pkg("quant.nvfp4")
+
+
+def test_nvfp4_global_direction_by_field():
+    """compressed-tensors' weight_global_scale divides, modelopt's weight_scale_2 multiplies
+    (python/minisgl/quant/nvfp4.py:70-93); an unknown field or a non-positive global is refused."""
+    g = torch.tensor(2688.0)
+    assert float(NV4.nvfp4_global_multiplier(g, global_field="weight_global_scale")) == float(1.0 / g)
+    assert float(NV4.nvfp4_global_multiplier(torch.tensor(2.078e-4), global_field="weight_scale_2")) == \
+        float(torch.tensor(2.078e-4))
+    with pytest.raises(ValueError, match="unknown"):
+        NV4.nvfp4_global_multiplier(g, global_field="global")
+    with pytest.raises(ValueError):
+        NV4.nvfp4_global_multiplier(torch.tensor(0.0), global_field="weight_scale_2")
+
+
+def test_nvfp4_split_is_byte_verbatim():
+    """The block scale passes through byte for byte (uint8 checkpoints are bitcast, not converted);
+    the global becomes an (N,) f32 multiplier vector."""
+    raw = torch.arange(0, 126, dtype=torch.uint8)[:120].reshape(8, 15)[:, :12].contiguous()
+    block, glob = NV4.split_nvfp4_scale(raw.reshape(8, 12), torch.tensor(4.0), global_field="weight_global_scale")
+    assert block.dtype == torch.float8_e4m3fn and torch.equal(block.view(torch.uint8), raw.reshape(8, 12))
+    assert glob.shape == (8,) and torch.all(glob == 0.25)
+    with pytest.raises(ValueError):
+        NV4.split_nvfp4_scale(raw.reshape(8, 12).to(torch.float16), torch.tensor(4.0), global_field="weight_scale_2")
+
+
+def test_nvfp4_post_load_layouts():
+    """Dense and grouped NVFP4 post-load: codes verbatim in the op layout, e4m3 scales group-major,
+    the global's f32 bits viewed as int32, and dequant_reference = lut * block * global."""
+    N, K = 64, 128
+    g = synth.gen(21)
+    codes = torch.randint(0, 16, (N, K), generator=g, dtype=torch.int32)
+    wpk = (codes[:, 0::2] | (codes[:, 1::2] << 4)).to(torch.uint8)
+    ws = (torch.rand(N, K // 16, generator=g) * 6 + 0.25).to(torch.float8_e4m3fn)
+    glob = torch.rand(N, generator=g) * 1e-3 + 1e-4
+    lay = SimpleNamespace(weight_packed=wpk, weight_scale=ws, weight_global=glob)
+    M_.NvFp4LinearMethod(NV).process_weights_after_load(lay)
+    assert torch.equal(_unpack_rows(lay._w_packed_op), codes)
+    assert torch.equal(lay._scales_op.view(torch.uint8), ws.t().contiguous().view(torch.uint8))
+    assert torch.equal(lay._global_op.view(torch.float32), glob)
+    deq = NV4.dequant_reference(wpk, ws, glob)
+    lut = torch.tensor(pkg("quant.mxfp4").FP4_E2M1_LUT)
+    want = lut[codes.long()] * ws.float().repeat_interleave(16, dim=1) * glob[:, None]
+    assert torch.equal(deq, want)
+    ex = L_.create_moe_quant_method(NV).create_experts(2, N, K)
+    ex.weight_packed.copy_(torch.stack([wpk, wpk]))
+    ex.weight_scale.copy_(torch.stack([ws, ws]))
+    ex.weight_global.copy_(torch.stack([glob, glob * 2]))
+    ex.post_load()
+    assert ex._scales_op.shape == (2, K // 16, N) and ex._zeros_op.dtype == torch.int32
+    assert torch.equal(ex._zeros_op[1].view(torch.float32), glob * 2)
