@@ -18,6 +18,9 @@ zero-point int4, M=16, K=2560, N=9728), cfg4 (MoE E=128 top-8 H=2048 I=768, T in
 and cfg5 (MXFP4 E8M0, K x N in {8192x28672, 28672x8192}, M in {1,16,4096}); GB/s against 8 TB/s
 for the decode sizes, TFLOPS against the 5 PFLOPS fp8 peak for the large ones.
 
+next_formats reports the W4A16 arm (unquantized activations) and NVFP4 through the same operator
+API (not BASELINE configs; the shapes are the gate_up ones above).
+
 producer_norm_step times the same sweep with its inputs coming out of the RMSNorm + residual-add
 producer: once with the linear quantizing its bf16 input, once with the producer's fp8 pair
 (no act-quant launches).
@@ -256,6 +259,61 @@ def configs_leg(kernels, dev) -> dict:
     return out
 
 
+def formats_leg(kernels, dev) -> dict:
+    """The formats beyond the BASELINE configs, through the same operator API: the W4A16 arm
+    (unquantized bf16 activations; GPTQ-sym int4 g128 at the gate_up shape K=4096, N=28672, M in
+    {1, 16, 2048}) and NVFP4 (e2m1 + e4m3 block-16 scales + per-channel global; W4A8 at the cfg5
+    gate_up shape K=8192, N=28672, M in {1, 16, 4096}, and W4A16 at M=1). Weights rotate over more
+    than twice the MALL for the bandwidth-bound sizes; bytes count codes, scales (and the NVFP4
+    global), bf16 activations in and out."""
+    import torch
+
+    out = {}
+    gen = torch.Generator(device=dev).manual_seed(13)
+    K, N, g = 4096, 28672, 128
+    copies = []
+    for _ in range(10):
+        t = kernels.repack_w4(_rand_words((N, K // 8), gen, dev))
+        sc = (torch.randn(K // g, N, generator=gen, device=dev).abs() * 0.02).to(torch.float16)
+        copies.append((t, sc))
+    for M in (1, 16):
+        x = make_x(M, K, 600 + M, dev)
+        us = _time_calls([lambda c=c: kernels.w4a16_linear(x, c[0], c[1], None, g, N) for c in copies], 40)
+        out[f"w4a16_int4_M{M}_K{K}_N{N}"] = _gbs(algo_bytes(M, K, N), us)
+    M = 2048
+    x = make_x(M, K, 602, dev)
+    c = copies[0]
+    us = _time_calls([lambda: kernels.w4a16_linear(x, c[0], c[1], None, g, N)], 5)
+    out[f"w4a16_int4_M{M}_K{K}_N{N}"] = _tflops(2.0 * M * N * K, us)
+    del copies
+    K, N = 8192, 28672
+    copies = []
+    for _ in range(5):
+        t = kernels.repack_w4(_rand_words((N, K // 8), gen, dev), weight_is_e2m1=True)
+        sc = (torch.rand(K // 16, N, generator=gen, device=dev) * 6 + 0.25).to(torch.float8_e4m3fn)
+        gl = torch.rand(N, generator=gen, device=dev) * 1e-3 + 1e-4
+        copies.append((t, sc, gl))
+    nv_bytes = lambda M: N * K // 2 + (K // 16) * N + N * 4 + M * K * 2 + M * N * 2
+    for M in (1, 16):
+        x = make_x(M, K, 700 + M, dev)
+        us = _time_calls([lambda c=c: kernels.w4a8_linear(x, c[0], c[1], c[2], 16, weight_is_e2m1=True)
+                          for c in copies], 40)
+        out[f"nvfp4_w4a8_M{M}_K{K}_N{N}"] = _gbs(nv_bytes(M), us)
+    x = make_x(1, K, 701, dev)
+    us = _time_calls([lambda c=c: kernels.w4a16_linear(x, c[0], c[1], c[2], 16, N, weight_is_e2m1=True)
+                      for c in copies], 40)
+    out[f"nvfp4_w4a16_M1_K{K}_N{N}"] = _gbs(nv_bytes(1), us)
+    M = 4096
+    x = make_x(M, K, 702, dev)
+    q, s = kernels.act_quant(x)
+    c = copies[0]
+    us = _time_calls([lambda: kernels.w4a8_linear(x, c[0], c[1], c[2], 16, weight_is_e2m1=True, x_fp8=q,
+                                                  act_scales=s)], 5)
+    out[f"nvfp4_w4a8_M{M}_K{K}_N{N}"] = _tflops(2.0 * M * N * K, us)
+    del copies
+    return out
+
+
 def producer_leg(kernels, dev, weights, steps: int = 100) -> dict:
     """The configs[1] sweep with its activations produced by the RMSNorm + residual-add producer, in
     two graph-replayed steps of 20 (norm, linear) pairs: `in_op_quant` runs rms_norm_add then
@@ -393,6 +451,7 @@ def main() -> int:
     prefill = None if args.no_prefill else prefill_leg(kernels, dev)
     others = None if args.no_configs else configs_leg(kernels, dev)
     producer = None if args.no_configs else producer_leg(kernels, dev, weights)
+    formats = None if args.no_configs else formats_leg(kernels, dev)
     cpu = None if args.no_cpu_baseline else cpu_baseline_leg()
 
     line = {
@@ -423,6 +482,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "prefill_config3": prefill,
         "other_configs": others,
+        "next_formats": formats,
         "producer_norm_step": producer,
     }
     print(json.dumps(line))

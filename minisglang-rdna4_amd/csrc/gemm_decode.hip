@@ -42,7 +42,8 @@ GemvPlan plan_gemv(const GemmArgs& p, int64_t row_blocks, bool quant_src) {
   pl.waves = (int)w;
   pl.tpw = (int)tpw;
 
-  const bool fast = (p.wfmt == kInt4 && p.group % kTileK == 0) || (p.wfmt == kE2M1 && p.sfmt == kScaleE8M0);
+  const bool fast = (p.wfmt == kInt4 && p.group % kTileK == 0) || (p.wfmt == kE2M1 && p.sfmt == kScaleE8M0) ||
+                    gemv_nvfp4(p);
   const int64_t lbytes = rows * (int64_t)stage_stride((int)KT);
   const bool lds_ok = fast && !p.sorted_ids && rows <= 4 && lbytes <= kStageLdsMax;
   const bool fuse_ok = rows == 1 || (rows == 2 && strips <= 512 && p.K <= 8192);

@@ -145,8 +145,22 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_prefill_kernel(const GemmAr
       }
     } else {
       const v8i half8 = splat8(kE4M3Half4);
+      // the tile's group scales, all loads issued before the first MFMA (each sub-group's MFMAs
+      // would otherwise wait on their own dependent load)
+      constexpr int SMAX = MODE == 3 ? 8 : 4;
+      float scv[SMAX][NSB];
 #pragma unroll
-      for (int ss = 0; ss < (MODE == 3 ? 8 : 4); ++ss) {
+      for (int ss = 0; ss < SMAX; ++ss) {
+        const bool in = ss < gpt && kbase + (int64_t)ss * (kTileK / gpt) < K;
+        const int64_t g = in ? (kbase + (int64_t)ss * (kTileK / gpt)) / group : 0;
+#pragma unroll
+        for (int j = 0; j < NSB; ++j) {
+          const int64_t n = strip[j] * kTileN + (lane & 15);
+          scv[ss][j] = (in && sval[j]) ? group_scale(scales, p.sfmt, g * N + n, zeros, n) : 0.f;
+        }
+      }
+#pragma unroll
+      for (int ss = 0; ss < SMAX; ++ss) {
         if (ss >= gpt || kbase + (int64_t)ss * (kTileK / gpt) >= K) break;
         const int msk = gpt == 1 ? 127 : subgroup_mask_scale(lane, gpt, ss);
         const int64_t g = (kbase + (int64_t)ss * (kTileK / gpt)) / group;
@@ -160,7 +174,7 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_prefill_kernel(const GemmAr
           const int64_t n = strip[j] * kTileN + (lane & 15);
           v8i b = MODE == 1 ? unpack_tile_int4(raw[j]) : fp4_operand(raw[j]);
           if (MODE == 3 && gpt == 8) b = fp4_half_operand(b, ss);
-          const float sc = sval[j] ? group_scale(scales, p.sfmt, g * N + n, zeros, n) : 0.f;
+          const float sc = scv[ss][j];
           float coef = -1.0f;
           if (MODE == 1 && zeros && sval[j]) {
             const uint32_t zw = (uint32_t)zeros[g * (N / 8) + n / 8];

@@ -148,7 +148,9 @@ __device__ __forceinline__ void gemv_tile(const GemmArgs& p, const v8i& a, const
 //   1: int4, group 32/64 (sub-tile groups, scales loaded per sub-group)
 //   2: e2m1 with E8M0 block scales (bytes preloaded, fed to the scaled MFMA)
 //   3: e2m1 with fp16 group scales (sub-tile groups)
-constexpr int kModeI4 = 0, kModeI4Sub = 1, kModeE8M0 = 2, kModeE2M1F16 = 3;
+//   4: NVFP4 (e2m1, e4m3 group-16 scales preloaded with the weights, per-channel global applied in
+//      the epilogue)
+constexpr int kModeI4 = 0, kModeI4Sub = 1, kModeE8M0 = 2, kModeE2M1F16 = 3, kModeNV = 4;
 
 // Where a wave's A fragments come from.
 //   kAGlobal: fp8 rows in global memory, loaded per tile with the weights (grouped rows, or blocks
@@ -175,7 +177,8 @@ __host__ __device__ inline int stage_stride(int KT) { return KT * kTileK + 16; }
 //   GPT: groups per K tile for the sub-tile-group modes (1 for the others).
 template <int NSTR, int CH, int MODE, int AMODE, bool SYM, int SM, int GPT>
 __global__ void __launch_bounds__(512) gemv_kernel(const GemmArgs p, int tpw) {
-  constexpr int WFMT = (MODE == kModeE8M0 || MODE == kModeE2M1F16) ? kE2M1 : kInt4;
+  constexpr int WFMT = (MODE == kModeE8M0 || MODE == kModeE2M1F16 || MODE == kModeNV) ? kE2M1 : kInt4;
+  static_assert(MODE != kModeNV || GPT == 8, "NVFP4 tiles hold 8 groups");
   constexpr bool kStaged = AMODE != kAGlobal;
   // grouped (MoE) rows only reach the global-A kernels: the staged and fused kernels are compiled
   // without the align lookups, so their prologue has no chain of dependent argument loads
@@ -213,7 +216,7 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemmArgs p, int tpw) {
   const uint4* wt = p.wt + (size_t)(expert * p.w_expert_tiles) * 64;
   // scale element size from the mode (E8M0 bytes, else fp16), so that the scale base stays in
   // scalar registers
-  const int kEsz = (MODE == kModeE8M0 || (MODE == kModeE2M1F16 && p.sfmt == kScaleE4M3)) ? 1 : 2;
+  const int kEsz = (MODE == kModeE8M0 || MODE == kModeNV || (MODE == kModeE2M1F16 && p.sfmt == kScaleE4M3)) ? 1 : 2;
   const void* scales = reinterpret_cast<const char*>(p.scales) + (size_t)(expert * p.s_expert_stride) * kEsz;
   const int32_t* zeros = p.zeros ? p.zeros + expert * p.z_expert_stride : nullptr;
   // 32-bit index math on the hot path (tile, scale and zero indices of one matrix fit easily)
@@ -263,6 +266,9 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemmArgs p, int tpw) {
   v2h sc[(CH + 1) / 2][NSTR];
   uint32_t zw[SYM ? 1 : CH][NSTR];
   int sb[CH][NSTR];
+  // NVFP4: the 8 group-scale bytes of a tile, two per register (loaded into the halves directly)
+  typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
+  v2u16 nvs[MODE == kModeNV ? CH : 1][NSTR][4];
   v4f acc[NSTR];
 #pragma unroll
   for (int j = 0; j < NSTR; ++j) acc[j] = zero4;
@@ -297,6 +303,12 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemmArgs p, int tpw) {
       } else if (MODE == kModeE8M0) {
         // blocks past K read as 0 (2^-127) from the descriptor's bound; their activations are 0
         sb[t][j] = (int)bload8(rs_s, (uint32_t)((lane >> 4) * N + n), (uint32_t)(kt * 4 * N));
+      } else if (MODE == kModeNV) {
+        // groups past K read as 0 from the descriptor's bound (a zero scale)
+#pragma unroll
+        for (int ss = 0; ss < 8; ++ss)
+          nvs[MODE == kModeNV ? t : 0][j][ss >> 1][ss & 1] =
+              (unsigned short)bload8(rs_s, (uint32_t)n, (uint32_t)((kt * 8 + ss) * N));
       }
     }
   };
@@ -418,6 +430,22 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemmArgs p, int tpw) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[j][r] += scf * (c[r] + coef * rh[r]);
       }
+    } else if (MODE == kModeNV) {
+      // 16-wide groups: each 32-element block of a lane's operand holds two groups, so each group
+      // is one MFMA on half the block (the other half zeroed) with only its block's scale open
+#pragma unroll
+      for (int j = 0; j < NSTR; ++j) {
+        if (!sval[j]) continue;
+        const v8i b = fp4_operand(raw[t][j]);
+#pragma unroll
+        for (int ss = 0; ss < 8; ++ss) {
+          const v4f c = mfma_f8f4_sb(at, fp4_half_operand(b, ss), zero4, subgroup_mask_scale(lane, 8, ss));
+          const v2u16 pr = nvs[MODE == kModeNV ? t : 0][j][ss >> 1];
+          const float scf = __builtin_amdgcn_cvt_f32_fp8((int)(uint32_t)pr[ss & 1], 0);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[j][r] += scf * c[r];
+        }
+      }
     } else {
       gemv_tile<NSTR, WFMT, GPT, SYM>(p, at, raw[t], sval, strip, kt, scales, zeros, lane, acc);
     }
@@ -445,7 +473,8 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemmArgs p, int tpw) {
 #pragma unroll
     for (int j = 0; j < NSTR; ++j) rawp[j] = wt[(strip_c[j] * KT + kfull) * 64 + lane];
     const v8i ap = load_a_operand(arow + kfull * kTileK, K - kfull * kTileK, lane);
-    gemv_tile<NSTR, WFMT, GPT, SYM>(p, ap, rawp, sval, strip, kfull, scales, zeros, lane, acc);
+    gemv_tile<NSTR, WFMT, GPT, SYM>(p, ap, rawp, sval, strip, kfull, scales, MODE == kModeNV ? nullptr : zeros, lane,
+                                    acc);
   }
 
   // Cross-wave reduction through LDS, over the block's existing rows only (row i = 4q + r of the
@@ -479,6 +508,15 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemmArgs p, int tpw) {
     }
     const float scl = srow[i];
     const int64_t row = m0 + i, col = sj * kTileN + c;
+    if (MODE == kModeNV) {
+      // the per-output-channel global (f32 bits in the zeros slot)
+      tot *= __int_as_float(zeros[col]);
+      if (p.silu) {
+        int64_t su;
+        strip_of(p.silu, sg, j + half, half, NSTR, nstrips, su);
+        tot_up *= __int_as_float(zeros[su * kTileN + c]);
+      }
+    }
     if (p.silu)
       store_out(p, row, col, silu_mul(tot * scl, tot_up * scl, p.out_dtype));
     else
@@ -506,6 +544,11 @@ bool launch_gemv_fused(const GemmArgs& p, dim3 grid, const GemvPlan& pl, hipStre
 // sub-tile groups (int4 group 32/64, e2m1 with fp16 scales), A read per tile
 bool launch_gemv_generic(const GemmArgs& p, dim3 grid, const GemvPlan& pl, hipStream_t stream);
 
+// NVFP4 (e2m1 weights, e4m3 group-16 scales, per-channel global): the fast path's dedicated mode
+inline bool gemv_nvfp4(const GemmArgs& p) {
+  return p.wfmt == kE2M1 && p.sfmt == kScaleE4M3 && p.group == 16 && p.zeros != nullptr;
+}
+
 // Chunk length (tiles per strip held in registers at once) of the sub-tile-group kernels: 4 for
 // short K ranges, else 8 (longer ranges roll the window through the range).
 inline int gemv_chunk(int tpw) { return tpw <= 4 ? 4 : 8; }
@@ -519,22 +562,23 @@ constexpr int kGemvChunk = 4;
 // Launch of one kernel variant; the staging depth only exists for staged A sources.
 template <int NS, int CHK, int MD, int AM, bool SY>
 void gemv_launch_sm(const GemmArgs& p, dim3 grid, dim3 block, size_t lds, hipStream_t stream, const GemvPlan& pl) {
+  constexpr int G = MD == kModeNV ? 8 : 1;
   if constexpr (AM == kAGlobal) {
-    hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 4, 1>), grid, block, lds, stream, p, pl.tpw);
+    hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 4, G>), grid, block, lds, stream, p, pl.tpw);
   } else if constexpr (AM == kAStage) {
     if (pl.sm <= 4)
-      hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 4, 1>), grid, block, lds, stream, p, pl.tpw);
+      hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 4, G>), grid, block, lds, stream, p, pl.tpw);
     else
-      hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 8, 1>), grid, block, lds, stream, p, pl.tpw);
+      hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 8, G>), grid, block, lds, stream, p, pl.tpw);
   } else {
     if (pl.sm == 1)
-      hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 1, 1>), grid, block, lds, stream, p, pl.tpw);
+      hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 1, G>), grid, block, lds, stream, p, pl.tpw);
     else if (pl.sm == 2)
-      hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 2, 1>), grid, block, lds, stream, p, pl.tpw);
+      hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 2, G>), grid, block, lds, stream, p, pl.tpw);
     else if (pl.sm == 4)
-      hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 4, 1>), grid, block, lds, stream, p, pl.tpw);
+      hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 4, G>), grid, block, lds, stream, p, pl.tpw);
     else
-      hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 8, 1>), grid, block, lds, stream, p, pl.tpw);
+      hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 8, G>), grid, block, lds, stream, p, pl.tpw);
   }
 }
 
@@ -546,13 +590,16 @@ bool launch_gemv_amode(const GemmArgs& p, dim3 grid, const GemvPlan& pl, hipStre
   const dim3 block(pl.waves * 64);
   const bool i4 = p.wfmt == kInt4 && p.group % kTileK == 0;
   const bool e8 = p.wfmt == kE2M1 && p.sfmt == kScaleE8M0;
-  if (!i4 && !e8) return AMODE == kAGlobal ? launch_gemv_generic(p, grid, pl, stream) : false;
+  const bool nv = gemv_nvfp4(p);
+  if (!i4 && !e8 && !nv) return AMODE == kAGlobal ? launch_gemv_generic(p, grid, pl, stream) : false;
 #define W4A8_GEMV_LAUNCH(NS, CHK)                                                                            \
   do {                                                                                                       \
     if (i4 && p.zeros == nullptr)                                                                            \
       gemv_launch_sm<NS, CHK, kModeI4, AMODE, true>(p, grid, block, lds, stream, pl);                        \
     else if (i4)                                                                                             \
       gemv_launch_sm<NS, CHK, kModeI4, AMODE, false>(p, grid, block, lds, stream, pl);                       \
+    else if (nv)                                                                                             \
+      gemv_launch_sm<NS, CHK, kModeNV, AMODE, false>(p, grid, block, lds, stream, pl);                       \
     else                                                                                                     \
       gemv_launch_sm<NS, CHK, kModeE8M0, AMODE, false>(p, grid, block, lds, stream, pl);                     \
     return true;                                                                                             \

@@ -300,9 +300,10 @@ __device__ __forceinline__ float load_scale(const void* scales, int fmt, int64_t
 }
 
 // group scale of output channel n: the stored scale, times the NVFP4 global (zeros slot, f32 bits)
+// when zeros is given (kernels that apply the global in their epilogue pass null)
 __device__ __forceinline__ float group_scale(const void* scales, int fmt, int64_t idx, const int32_t* zeros, int64_t n) {
   const float s = load_scale(scales, fmt, idx);
-  return fmt == kScaleE4M3 ? s * __int_as_float(zeros[n]) : s;
+  return (fmt == kScaleE4M3 && zeros) ? s * __int_as_float(zeros[n]) : s;
 }
 
 }  // namespace w4a8
