@@ -12,7 +12,9 @@
  *   - no entry point allocates: outputs and workspaces come from the caller, so every launch is
  *     capturable into a HIP graph as long as its pointers stay fixed;
  *   - dtype codes: 0 = bf16, 1 = fp16, 2 = f32. Scale formats: 0 = fp16 group scales,
- *     1 = E8M0 (uint8) 32-element block scales. Weight formats: 0 = int4 codes, 1 = e2m1 codes.
+ *     1 = E8M0 (uint8) 32-element block scales, 2 = NVFP4 e4m3 (uint8) 16-element block scales
+ *     with the per-output-channel f32 global in the zeros slot (its bits as int32; (N,) per
+ *     matrix, (E, N) for experts). Weight formats: 0 = int4 codes, 1 = e2m1 codes.
  *
  * Data layouts (all row-major):
  *   x_fp8 (M, ldx) uint8 e4m3fn codes; act_scales (M,) f32.
@@ -34,6 +36,10 @@ extern "C" {
 #define W4A8_ERR_INVALID 1
 #define W4A8_ERR_UNSUPPORTED 2
 #define W4A8_ERR_HIP 3
+
+#define W4A8_SCALE_F16 0
+#define W4A8_SCALE_E8M0 1
+#define W4A8_SCALE_E4M3 2
 
 /* ABI revision (1). */
 int w4a8_abi_version(void);
