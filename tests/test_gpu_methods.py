@@ -216,3 +216,40 @@ def test_nvfp4_moe_method_matches_operator(kernels, dev):
                            weight_is_e2m1=True)
     torch.cuda.synchronize()
     assert torch.equal(out, ref)
+
+
+def test_loader_builds_serving_layers(kernels, dev, tmp_path):
+    """Checkpoint tensors -> quant.loader -> method.apply on the GPU, bit-identical to the operator
+    called on the same tensors converted by hand (AWQ gate_up from two parts, NVFP4 modelopt leaf)."""
+    from safetensors.torch import save_file
+    LD = pkg("quant.loader")
+    K, I, g = 512, 128, 128
+    gen = synth.gen(95)
+    t = {}
+    for p in ("gate_proj", "up_proj"):
+        t[f"m.{p}.qweight"] = _rand_i32((K, I // 8), gen)
+        t[f"m.{p}.scales"] = (torch.rand(K // g, I, generator=gen) * 0.02 + 1e-3).to(torch.float16)
+        t[f"m.{p}.qzeros"] = _rand_i32((K // g, I // 8), gen)
+    codes = torch.randint(0, 256, (I, K // 2), generator=gen, dtype=torch.int32).to(torch.uint8)
+    t["n.weight"] = codes
+    t["n.weight_scale"] = (torch.rand(I, K // 16, generator=gen) * 4 + 0.5).to(torch.float8_e4m3fn)
+    t["n.weight_scale_2"] = torch.tensor(2e-3)
+    save_file(t, str(tmp_path / "c.safetensors"))
+    tensors = LD.read_safetensors([tmp_path / "c.safetensors"])
+    m, lay = LD.build_linear(AWQ, "m.gate_up_proj", K, 2 * I, tensors, parts=["m.gate_proj", "m.up_proj"], device=dev)
+    x = synth.activations(3, K, seed=1).to(dev)
+    ops = [kernels.awq_to_op_layout(t[f"m.{p}.qweight"], t[f"m.{p}.scales"], t[f"m.{p}.qzeros"]) for p in ("gate_proj", "up_proj")]
+    w = torch.cat([o[0] for o in ops], 0).to(dev)
+    s = torch.cat([o[1] for o in ops], 1).to(dev)
+    z = torch.cat([o[2] for o in ops], 1).to(dev)
+    assert torch.equal(m.apply(lay, x, None), kernels.w4a8_linear(x, w, s, z, g))
+    assert torch.equal(m.apply_swiglu(lay, x), kernels.w4a8_linear_silu(x, w, s, z, g))
+    NV_ = C_.QuantConfig.from_hf({"quantization_config": {"quant_method": "modelopt", "quant_algo": "NVFP4"}})
+    mn, ln = LD.build_linear(NV_, "n", K, I, tensors, device=dev)
+    nv4 = pkg("quant.nvfp4")
+    conv = nv4.convert_nvfp4_weight(codes, t["n.weight_scale"])
+    glob = torch.full((I,), float(torch.tensor(2e-3)), dtype=torch.float32, device=dev)
+    ref = kernels.w4a8_linear(x, conv["w_packed"].to(dev), conv["scales"].t().contiguous().to(dev), glob, 16,
+                              weight_is_e2m1=True)
+    torch.cuda.synchronize()
+    assert torch.equal(mn.apply(ln, x, None), ref)
