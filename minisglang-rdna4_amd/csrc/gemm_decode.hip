@@ -7,10 +7,12 @@ namespace w4a8 {
 
 // Shape policy (from launch-shape sweeps on MI355X at the Llama-3-8B decode shapes, M = 1..16).
 //   * nstr: blocks of more than 4 rows read A per tile from global memory and share each A
-//     fragment between two strips; smaller blocks run one strip per wave.
-//   * waves x tpw: up to 8 waves per workgroup owning at least 4 K tiles each (many short waves
-//     keep more loads in flight than few long ones); wide weights whose grid would pass ~8192
-//     waves get fewer, longer waves instead (a grid that large runs in several rounds).
+//     fragment between two strips when the weight has 384+ strips; smaller blocks, and narrower
+//     dense weights (whose two-strip grid would leave CUs idle), run one strip per wave.
+//   * waves x tpw: up to 8 waves per workgroup (4 for dense two-strip grids of 512+ blocks) owning at least 4 K
+//     tiles each (many short waves keep more loads in flight than few long ones); wide weights
+//     whose grid would pass ~8192 waves get fewer, longer waves instead (a grid that large runs in
+//     several rounds).
 //   * A source: up to 4 rows are staged in LDS (fp8 codes, one barrier). A one-row call on
 //     bf16/fp16 input, or a two-row call on a narrow weight, quantizes its rows in the GEMV itself
 //     (one launch instead of two); larger blocks re-read and re-quantize too many rows per
@@ -22,9 +24,14 @@ GemvPlan plan_gemv(const GemmArgs& p, int64_t row_blocks, bool quant_src) {
   const int64_t KT = (p.K + kTileK - 1) / kTileK;
   const int64_t rows = p.sorted_ids ? 16 : (p.M < 16 ? p.M : 16);
   const int64_t strips = p.N / kTileN;
-  pl.nstr = rows > 4 ? 2 : 1;
+  // two strips per workgroup only where that still leaves about a workgroup per CU (384+ strips);
+  // narrower dense weights (o_proj, down at 4096 channels) run one strip each, twice the grid
+  // (grouped MoE calls keep two: their grids already span the routed experts)
+  pl.nstr = rows > 4 && (p.sorted_ids || strips >= 384) ? 2 : 1;
+  // dense two-strip grids of 512+ workgroups (gate_up): at most 4 waves of longer K ranges
+  const int64_t wmax = (pl.nstr == 2 && !p.sorted_ids && (strips + 1) / 2 * row_blocks >= 512) ? 4 : 8;
   int64_t w = (KT + 3) / 4;
-  if (w > 8) w = 8;
+  if (w > wmax) w = wmax;
   if (w < 1) w = 1;
   const int64_t groups = (strips + pl.nstr - 1) / pl.nstr * row_blocks;
   while (w > 1 && groups * w > 8192 && (KT + w - 1) / w < 8) w = (w + 1) / 2;
