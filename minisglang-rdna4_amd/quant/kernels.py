@@ -40,6 +40,8 @@ MOE_W4A16 = os.environ.get("MINISGL_MOE_W4A16", "0")
 _MOE_GEMM1_GEMV_MAX = 32
 _MOE_WMMA_DIM = 16
 _MOE_BLOCK_M_CHOICES = (16, 32, 64, 128)
+# routed rows per expert up to which w4a8_moe runs the skinny grouped GEMV (block_m 16)
+_MOE_SKINNY_MAX_ROWS = 40
 
 
 # --------------------------------------------------------------------------------------------
@@ -473,6 +475,20 @@ def _moe_block_m(num_tokens: int, num_experts: int, top_k: int, flag_gemm1: bool
     return max(bm, wide)
 
 
+def _moe_block_m_auto(num_tokens: int, num_experts: int, top_k: int) -> int:
+    """The tile height w4a8_moe picks when the caller gives none, from MI355X measurements of these
+    kernels at the configs[4] shape (E=128, top-8, H=2048, I=768): the skinny grouped GEMV (16-row
+    blocks) up to 40 routed rows per expert, where it streams each expert's weights once per 16
+    rows (T=256: 124 us, against 203 us with the 64-row tiles the reference's rule picks there);
+    128-row MFMA tiles above (T=1024: 263 us, against 320 us at 64). The reference raises to 64
+    past 32 tokens because its own GEMV arm loses there (``_moe_block_m``, kept as written for
+    callers and tests that want that rule). ``MINISGL_MOE_BLOCK_M`` still forces a value."""
+    if os.environ.get("MINISGL_MOE_BLOCK_M"):
+        return _moe_block_m(num_tokens, num_experts, top_k)
+    rows_per_expert = (num_tokens * top_k) / max(num_experts, 1)
+    return 16 if rows_per_expert <= _MOE_SKINNY_MAX_ROWS else 128
+
+
 def _route_align(gating_output: torch.Tensor, top_k: int, renormalize: bool, num_experts: int,
                  block_size: int):
     """softmax + top-k + renormalize + align in one call (python/minisgl/quant/kernels.py:423-447).
@@ -663,7 +679,7 @@ def _moe_forward(x, w13, w13_scales, w13_zeros, w2, w2_scales, w2_zeros, gating_
         raise AssertionError(f"w4a8_moe: w2 has {H2} output channels, expected hidden size {K}")
     _grp2 = inter // w2_scales.shape[1]
     if block_m is None:
-        block_m = _moe_block_m(M, E, top_k, flag_gemm1=True)
+        block_m = _moe_block_m_auto(M, E, top_k)
 
     if x_fp8 is not None:
         assert act_scales is not None, "w4a8_moe: x_fp8 and act_scales must be supplied together"
