@@ -283,6 +283,15 @@ gemm_dma_kernel(const GemmArgs p) {
               else
                 acc[rb][j - 1][r] += scp * (cp[rb][r] + cfp * pre[rb][r]);
             }
+          // issue the previous strip's scale FMAs between this strip's MFMAs (one MFMA, then four
+          // VALU ops), so they run while the matrix pipe works instead of after it
+          if (j < NSB) {
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) {
+              __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+              __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+            }
+          }
         }
         if (j < NSB) {
 #pragma unroll
