@@ -552,7 +552,8 @@ inline bool gemv_nvfp4(const GemmArgs& p) {
 // Chunk length (tiles per strip held in registers at once) of the sub-tile-group kernels: 4 for
 // short K ranges, else 8 (longer ranges roll the window through the range).
 inline int gemv_chunk(int tpw) { return tpw <= 4 ? 4 : 8; }
-// The fast-path kernels always roll a 4-tile window. Measured on MI355X at the Llama-3-8B decode
+// The fast-path kernels roll a 4-tile window (3 for int4 with the fused-quant A source, see the
+// launch dispatch below). Measured on MI355X at the Llama-3-8B decode
 // shapes (one row): against an 8-tile window it costs fewer VGPRs (68 against 80, so seven waves
 // per SIMD and the whole gate_up grid resident at once instead of two rounds), and it queues fewer
 // weight loads ahead of each wave's A loads on the CU, so A is ready sooner; gate_up 15.5 us
@@ -592,12 +593,18 @@ bool launch_gemv_amode(const GemmArgs& p, dim3 grid, const GemvPlan& pl, hipStre
   const bool e8 = p.wfmt == kE2M1 && p.sfmt == kScaleE8M0;
   const bool nv = gemv_nvfp4(p);
   if (!i4 && !e8 && !nv) return AMODE == kAGlobal ? launch_gemv_generic(p, grid, pl, stream) : false;
+  // int4 with the fused-quant source keeps 3 tiles per wave in flight: its weight loads queue ahead
+  // of the activation row every workgroup reads before its first MFMA, and a smaller first burst
+  // gets that row in sooner (gate_up M=1: 15.2 -> 14.8 us). The e2m1 formats, with twice the bytes
+  // per row, measured slower with 3 (MXFP4 M=1: 23.8 -> 25.1 us) and keep 4. The window does not
+  // change the summation order.
+  constexpr int kChI4 = AMODE == kAQuant ? 3 : kGemvChunk;
 #define W4A8_GEMV_LAUNCH(NS, CHK)                                                                            \
   do {                                                                                                       \
     if (i4 && p.zeros == nullptr)                                                                            \
-      gemv_launch_sm<NS, CHK, kModeI4, AMODE, true>(p, grid, block, lds, stream, pl);                        \
+      gemv_launch_sm<NS, kChI4, kModeI4, AMODE, true>(p, grid, block, lds, stream, pl);                      \
     else if (i4)                                                                                             \
-      gemv_launch_sm<NS, CHK, kModeI4, AMODE, false>(p, grid, block, lds, stream, pl);                       \
+      gemv_launch_sm<NS, kChI4, kModeI4, AMODE, false>(p, grid, block, lds, stream, pl);                     \
     else if (nv)                                                                                             \
       gemv_launch_sm<NS, CHK, kModeNV, AMODE, false>(p, grid, block, lds, stream, pl);                       \
     else                                                                                                     \
