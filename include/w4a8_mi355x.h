@@ -152,6 +152,22 @@ int w4a8_moe_gemm(const uint8_t* a_fp8, int64_t lda, const float* a_scales, int 
 int w4a8_moe_combine(const float* y, int64_t ldy, const int32_t* inv_pos, const float* topk_w, int64_t T, int top_k,
                      int64_t H, void* out, int out_dtype, void* stream);
 
+/* Fused gemm2 + top-k weighted combine of the MoE FFN for decode-sized batches: replaces
+ * fp8_wmma.mmq_fp8_moe_gemm2_gather_reduce (python/minisgl/quant/kernels.py:831-850), one launch for
+ * the per-row act quant of the gemm1 buffer, gemm2 and the combine. a: the gemm1 buffer (P, K)
+ * bf16/fp16 at padded positions (row stride lda elements, 16-byte aligned); slot s = t*top_k + j of
+ * token t reads row inv_pos[s] (inv_pos < 0: dropped slot) with expert topk_ids[s], quantized per
+ * row as w4a8_act_quant does, bit for bit. out (T, N) = sum_j topk_w[t, j] * gemm2(row of slot
+ * (t, j)) in f32 over the slots in order, cast to out_dtype: the same bits as w4a8_act_quant +
+ * w4a8_moe_gemm (decode arm, block_m) + w4a8_moe_combine. Deterministic; no workspace, no atomics.
+ * Formats: int4 with groups of 128+, MXFP4 (E8M0) and NVFP4; K % 128 == 0, K <= 2048, top_k <= 16
+ * (w4a8_moe_gemm2_combine_supported), else kErrUnsupported (2). */
+int w4a8_moe_gemm2_combine_supported(int64_t K, int scale_fmt, int has_zeros, int wfmt, int64_t group_size, int top_k);
+int w4a8_moe_gemm2_combine(const void* a, int a_dtype, int64_t lda, const int32_t* topk_ids, const float* topk_w,
+                           const int32_t* inv_pos, int64_t T, int top_k, int block_m, int64_t P, const void* w_tile,
+                           int64_t E, int64_t N, int64_t K, const void* scales, int scale_fmt, const int32_t* zeros,
+                           int wfmt, int64_t group_size, void* out, int out_dtype, int64_t ldo, void* stream);
+
 /* ---- W4A16: the same 4-bit weights against unquantized bf16/fp16 activations. */
 
 /* Exact split of bf16/fp16 rows into fp8-e4m3 terms with power-of-two scales: row t of token m

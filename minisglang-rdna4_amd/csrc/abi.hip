@@ -14,6 +14,10 @@ int launch_act_quant(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx
 int launch_repack(const int32_t* w, int64_t N, int64_t K, int wfmt, void* out, hipStream_t stream);
 int launch_gemv(GemmArgs p, int64_t row_blocks, bool quant_src, hipStream_t stream);
 bool gemv_can_fuse_quant(const GemmArgs& p, int64_t row_blocks);
+bool moe_gemm2_combine_fits(int64_t K, int scale_fmt, bool has_zeros, int wfmt, int64_t group, int top_k);
+int launch_moe_gemm2_combine(const GemmArgs& p, int64_t row_blocks, const uint16_t* a, int64_t lda, int adtype,
+                             const int32_t* inv_pos, const int32_t* ids, const float* tw, int64_t T, int E,
+                             hipStream_t stream);
 size_t gemv_workspace_bytes(int64_t M, int64_t N, int64_t K, int grouped, int64_t row_blocks);
 int launch_prefill(const GemmArgs& p, int64_t rows_to_cover, int bm_rows, hipStream_t stream);
 int launch_prefill_lds(const GemmArgs& p, int64_t rows_to_cover, int bm_rows, hipStream_t stream);
@@ -54,6 +58,11 @@ static int hip_status(int rc, const char* what) {
   hipError_t e = hipGetLastError();
   return fail(kErrHip, "%s: HIP launch failed (%s)", what, hipGetErrorString(e));
 }
+
+namespace w4a8 {
+// the library's error slot, for entry points defined in other units
+int set_last_error(int code, const char* msg) { return fail(code, "%s", msg); }
+}  // namespace w4a8
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
@@ -425,6 +434,49 @@ int w4a8_moe_gemm(const uint8_t* a_fp8, int64_t lda, const float* a_scales, int 
   rc = launch_prefill_lds(p, nblk * block_m, bm_rows, (hipStream_t)stream);
   if (rc == kErrUnsupported) rc = launch_prefill(p, nblk * block_m, bm_rows, (hipStream_t)stream);
   return hip_status(rc, "w4a8_moe_gemm(prefill)");
+}
+
+int w4a8_moe_gemm2_combine_supported(int64_t K, int scale_fmt, int has_zeros, int wfmt, int64_t group_size, int top_k) {
+  return moe_gemm2_combine_fits(K, scale_fmt, has_zeros != 0, wfmt, group_size, top_k) ? 1 : 0;
+}
+
+int w4a8_moe_gemm2_combine(const void* a, int a_dtype, int64_t lda, const int32_t* topk_ids, const float* topk_w,
+                           const int32_t* inv_pos, int64_t T, int top_k, int block_m, int64_t P, const void* w_tile,
+                           int64_t E, int64_t N, int64_t K, const void* scales, int scale_fmt, const int32_t* zeros,
+                           int wfmt, int64_t group_size, void* out, int out_dtype, int64_t ldo, void* stream) {
+  const char* who = "w4a8_moe_gemm2_combine";
+  int rc = check_weights(who, N, K, scale_fmt, zeros, wfmt, group_size);
+  if (rc) return rc;
+  if (E <= 0 || E > 512) return fail(kErrUnsupported, "%s: num_experts=%lld outside [1, 512]", who, (long long)E);
+  if (block_m <= 0 || block_m % 16 || block_m >= 64)
+    return fail(kErrInvalid, "%s: the decode arm needs block_m in {16, 32, 48} (got %d)", who, block_m);
+  if (a_dtype != kBF16 && a_dtype != kF16) return fail(kErrInvalid, "%s: the gemm1 buffer must be bf16 or fp16", who);
+  if (lda < K || lda % 8 || !aligned16(a))
+    return fail(kErrInvalid, "%s: gemm1 buffer rows must be 16-byte aligned with stride >= K (lda=%lld)", who, (long long)lda);
+  if (out_dtype != kBF16 && out_dtype != kF16 && out_dtype != kF32) return fail(kErrInvalid, "%s: unknown output dtype", who);
+  if (ldo < N) return fail(kErrInvalid, "%s: ldo=%lld < N=%lld", who, (long long)ldo, (long long)N);
+  if (T < 0 || T > 65535 || top_k <= 0) return fail(kErrInvalid, "%s: T=%lld (at most 65535) top_k=%d", who, (long long)T, top_k);
+  const int64_t numel = T * top_k;
+  if (int rc2 = check_align(who, numel, E, block_m, P)) return rc2;
+  if (!topk_ids || !topk_w || !inv_pos) return fail(kErrInvalid, "%s: topk_ids, topk_w and inv_pos are required", who);
+  if (!moe_gemm2_combine_fits(K, scale_fmt, zeros != nullptr, wfmt, group_size, top_k))
+    return fail(kErrUnsupported, "%s: K=%lld, group %lld, formats %d/%d, top_k %d take the unfused path", who,
+                (long long)K, (long long)group_size, wfmt, scale_fmt, top_k);
+  if (numel == 0) return kOk;
+  // the grouped gemm2 this call replaces, for its K split
+  GemmArgs p = {};
+  p.M = P; p.N = N; p.K = K; p.KT = (K + 127) / 128;
+  p.wt = reinterpret_cast<const uint4*>(w_tile);
+  p.scales = scales; p.sfmt = scale_fmt; p.zeros = zeros; p.group = (int)group_size; p.wfmt = wfmt;
+  p.sorted_ids = topk_ids;  // non-null marks the grouped plan; the plan reads no array
+  p.top_k = top_k; p.num_slots = numel; p.bm = block_m;
+  p.w_expert_tiles = (N / 16) * p.KT;
+  p.s_expert_stride = (K / group_size) * N;
+  p.z_expert_stride = scale_fmt == kScaleE4M3 ? N : (K / group_size) * (N / 8);
+  p.out = out; p.out_dtype = out_dtype; p.ldo = ldo;
+  const int64_t rb = moe_max_blocks(numel, E, block_m, P) * block_m / 16;
+  return hip_status(launch_moe_gemm2_combine(p, rb, reinterpret_cast<const uint16_t*>(a), lda, a_dtype, inv_pos,
+                                             topk_ids, topk_w, T, (int)E, (hipStream_t)stream), who);
 }
 
 int w4a8_moe_combine(const float* y, int64_t ldy, const int32_t* inv_pos, const float* topk_w, int64_t T, int top_k,

@@ -9,16 +9,41 @@ namespace w4a8 {
 //   * nstr: blocks of more than 4 rows read A per tile from global memory and share each A
 //     fragment between two strips when the weight has 384+ strips; smaller blocks, and narrower
 //     dense weights (whose two-strip grid would leave CUs idle), run one strip per wave.
-//   * waves x tpw: up to 8 waves per workgroup (4 for dense two-strip grids of 512+ blocks) owning at least 4 K
-//     tiles each (many short waves keep more loads in flight than few long ones); wide weights
-//     whose grid would pass ~8192 waves get fewer, longer waves instead (a grid that large runs in
-//     several rounds).
+//   * waves x tpw: up to 8 waves per workgroup owning at least 4 K tiles each (many short waves
+//     keep more loads in flight than few long ones); wide weights whose grid would pass ~8192
+//     waves get fewer, longer waves instead (a grid that large runs in several rounds). Dense
+//     calls plan this from (N, K) alone (see plan_gemv).
 //   * A source: up to 4 rows are staged in LDS (fp8 codes, one barrier). A one-row call on
 //     bf16/fp16 input, or a two-row call on a narrow weight, quantizes its rows in the GEMV itself
 //     (one launch instead of two); larger blocks re-read and re-quantize too many rows per
 //     workgroup, so they take the act-quant kernel first.
-// The per-channel arithmetic depends only on (waves, tpw), which come from (M, N, K, row_blocks)
-// alone: the fused-silu arm, the plain arm and every A source agree bit for bit.
+// The per-channel arithmetic depends only on (waves, tpw). For dense calls they come from (N, K)
+// alone, planned as for a one-row call, so a row's output bits do not depend on how many rows share
+// the call (rows[0:m] alone == rows[0:m] inside a 16-row call); the fused-silu arm, the plain arm
+// and every A source agree bit for bit. Grouped (MoE) calls plan from their grid.
+//
+// K split of a grid of `groups` workgroups: up to 8 waves owning at least 4 K tiles each; grids
+// that would pass ~8192 waves get fewer, longer waves; grids of under ~2 waves per SIMD (the MoE
+// decode calls over a handful of experts, narrow dense weights) halve the tiles per wave, down to
+// 2 and up to 8 waves, so more of the weight bytes are in flight at once.
+static void plan_ksplit(int64_t KT, int64_t groups, int64_t& waves, int64_t& tpw) {
+  int64_t w = (KT + 3) / 4;
+  if (w > 8) w = 8;
+  if (w < 1) w = 1;
+  while (w > 1 && groups * w > 8192 && (KT + w - 1) / w < 8) w = (w + 1) / 2;
+  int64_t t = (KT + w - 1) / w;
+  w = (KT + t - 1) / t;
+  while (groups * w < 2048 && w < 8) {
+    const int64_t t2 = (t + 1) / 2;
+    const int64_t w2 = (KT + t2 - 1) / t2;
+    if (t2 < 2 || w2 > 8) break;
+    t = t2;
+    w = w2;
+  }
+  waves = w;
+  tpw = t;
+}
+
 GemvPlan plan_gemv(const GemmArgs& p, int64_t row_blocks, bool quant_src) {
   GemvPlan pl;
   const int64_t KT = (p.K + kTileK - 1) / kTileK;
@@ -28,24 +53,10 @@ GemvPlan plan_gemv(const GemmArgs& p, int64_t row_blocks, bool quant_src) {
   // narrower dense weights (o_proj, down at 4096 channels) run one strip each, twice the grid
   // (grouped MoE calls keep two: their grids already span the routed experts)
   pl.nstr = rows > 4 && (p.sorted_ids || strips >= 384) ? 2 : 1;
-  // dense two-strip grids of 512+ workgroups (gate_up): at most 4 waves of longer K ranges
-  const int64_t wmax = (pl.nstr == 2 && !p.sorted_ids && (strips + 1) / 2 * row_blocks >= 512) ? 4 : 8;
-  int64_t w = (KT + 3) / 4;
-  if (w > wmax) w = wmax;
-  if (w < 1) w = 1;
-  const int64_t groups = (strips + pl.nstr - 1) / pl.nstr * row_blocks;
-  while (w > 1 && groups * w > 8192 && (KT + w - 1) / w < 8) w = (w + 1) / 2;
-  int64_t tpw = (KT + w - 1) / w;
-  w = (KT + tpw - 1) / tpw;
-  // grids of under ~2 waves per SIMD (the MoE decode calls, a handful of experts): halve the tiles
-  // per wave, down to 2 and up to 8 waves, so more of the weight bytes are in flight at once
-  while (groups * w < 2048 && w < 8) {
-    const int64_t t2 = (tpw + 1) / 2;
-    const int64_t w2 = (KT + t2 - 1) / t2;
-    if (t2 < 2 || w2 > 8) break;
-    tpw = t2;
-    w = w2;
-  }
+  // dense: the one-row grid (one strip per workgroup, one row block); grouped: the launched grid
+  const int64_t split_groups = p.sorted_ids ? (strips + pl.nstr - 1) / pl.nstr * row_blocks : strips;
+  int64_t w, tpw;
+  plan_ksplit(KT, split_groups, w, tpw);
   pl.waves = (int)w;
   pl.tpw = (int)tpw;
 
@@ -88,10 +99,19 @@ int launch_gemv(GemmArgs p, int64_t row_blocks, bool quant_src, hipStream_t stre
   return hipGetLastError() == hipSuccess ? kOk : kErrHip;
 }
 
+// K split (waves, tpw) the grouped GEMV runs for these arguments and row blocks; the fused gemm2 +
+// combine reproduces it so that its per-slot rows equal the grouped gemm2's bit for bit.
+void gemv_ksplit(const GemmArgs& p, int64_t row_blocks, int& waves, int& tpw) {
+  const GemvPlan pl = plan_gemv(p, row_blocks, false);
+  waves = pl.waves;
+  tpw = pl.tpw;
+}
+
 // True when launch_gemv can quantize bf16/fp16 rows itself for this call.
 bool gemv_can_fuse_quant(const GemmArgs& p, int64_t row_blocks) {
   return plan_gemv(p, row_blocks, true).amode == kAQuant;
 }
+
 
 // The decode kernel reduces inside the workgroup: no workspace.
 size_t gemv_workspace_bytes(int64_t, int64_t, int64_t, int, int64_t) { return 0; }

@@ -416,7 +416,7 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemmArgs p, int tpw) {
         const v4f c = mfma_f8f8(at, unpack_tile_int4(raw[t][j]), seed);
         const float scf = f16_to_f32(sc[t >> 1][j][t & 1]);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[j][r] += scf * c[r];
+        for (int r = 0; r < 4; ++r) acc[j][r] = fmaf(scf, c[r], acc[j][r]);
       }
     } else if (MODE == kModeI4) {
       const v4f rh = mfma_f8f8(at, splat8(kE4M3Half4), zero4);
@@ -428,7 +428,7 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemmArgs p, int tpw) {
         const float coef = 15.0f - 2.0f * (float)((zw[SYM ? 0 : t][j] >> (4 * (n & 7))) & 15u);
         const float scf = f16_to_f32(sc[t >> 1][j][t & 1]);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[j][r] += scf * (c[r] + coef * rh[r]);
+        for (int r = 0; r < 4; ++r) acc[j][r] = fmaf(scf, fmaf(coef, rh[r], c[r]), acc[j][r]);
       }
     } else if (MODE == kModeNV) {
       // 16-wide groups: each 32-element block of a lane's operand holds two groups, so each group
@@ -443,7 +443,7 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemmArgs p, int tpw) {
           const v2u16 pr = nvs[MODE == kModeNV ? t : 0][j][ss >> 1];
           const float scf = __builtin_amdgcn_cvt_f32_fp8((int)(uint32_t)pr[ss & 1], 0);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) acc[j][r] += scf * c[r];
+          for (int r = 0; r < 4; ++r) acc[j][r] = fmaf(scf, c[r], acc[j][r]);
         }
       }
     } else {
@@ -543,6 +543,8 @@ bool launch_gemv_staged(const GemmArgs& p, dim3 grid, const GemvPlan& pl, hipStr
 bool launch_gemv_fused(const GemmArgs& p, dim3 grid, const GemvPlan& pl, hipStream_t stream);
 // sub-tile groups (int4 group 32/64, e2m1 with fp16 scales), A read per tile
 bool launch_gemv_generic(const GemmArgs& p, dim3 grid, const GemvPlan& pl, hipStream_t stream);
+// K split (waves, tiles per wave) the GEMV runs for these arguments and row blocks
+void gemv_ksplit(const GemmArgs& p, int64_t row_blocks, int& waves, int& tpw);
 
 // NVFP4 (e2m1 weights, e4m3 group-16 scales, per-channel global): the fast path's dedicated mode
 inline bool gemv_nvfp4(const GemmArgs& p) {

@@ -300,10 +300,11 @@ moe_combine_kernel(const float* __restrict__ y, int64_t ldy, const int32_t* __re
       if (pos >= 0) {
         const float w = tw[t * top_k + j];
         const float4 v = *reinterpret_cast<const float4*>(y + pos * ldy + h);
-        acc.x += w * v.x;
-        acc.y += w * v.y;
-        acc.z += w * v.z;
-        acc.w += w * v.w;
+        // one FMA per slot, in slot order (the fused gemm2 + combine does the same)
+        acc.x = fmaf(w, v.x, acc.x);
+        acc.y = fmaf(w, v.y, acc.y);
+        acc.z = fmaf(w, v.z, acc.z);
+        acc.w = fmaf(w, v.w, acc.w);
       }
     }
     if (dtype == kF32) {

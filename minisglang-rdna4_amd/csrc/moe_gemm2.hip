@@ -1,0 +1,246 @@
+// Fused gemm2 + top-k weighted combine of the MoE FFN for decode-sized batches: one launch does
+// the per-row act quant of the gemm1 buffer, the down projection and the per-token reduction.
+// Restates fp8_wmma.mmq_fp8_moe_gemm2_gather_reduce (python/minisgl/quant/kernels.py:831-850):
+//   out[t, n] = sum_j tw[t, j] * s_(t,j) * sum_g scale[e, g, n] * sum_{k in g} e4m3(q_(t,j)[k]) * w_e(n, k)
+// with q_(t,j), s_(t,j) the per-row fp8 quant of the gemm1 row of slot (t, j) (act_quant.h's
+// arithmetic) and e the slot's expert; f32 throughout, cast to the output dtype once.
+//
+// Work split: workgroup = (16-channel strip, token), one wave per top-k slot. Each wave quantizes
+// its slot's gemm1 row into LDS, streams its expert's weight tiles for the strip and leaves the
+// slot's 16 outputs in LDS; then 16 threads sum the token's slots in slot order. No workgroup
+// talks to another, so there are no atomics and no device-scope fences, and the result does not
+// depend on timing. Experts shared by several tokens are read once per token (from L2 or MALL
+// after the first): the grid's strips map to XCDs by strip index, so every token's workgroup for
+// a strip meets the same L2.
+//
+// Bits: a slot's row sum follows the grouped gemm2's K split (K tiles in runs of tpw, one
+// accumulator per run started from zero, the runs summed in order) with the same per-tile MFMA
+// and FMA sequence, and the combine is the unfused combine's FMA chain, so the output equals the
+// unfused path (act quant, w4a8_moe_gemm decode arm, w4a8_moe_combine) bit for bit.
+#include "gemv.h"
+
+namespace w4a8 {
+
+struct G2CArgs {
+  const uint16_t* a;      // gemm1 buffer (P, K) bf16/fp16, rows at padded positions
+  int64_t lda;            // elements
+  int adtype;
+  const int32_t* inv_pos; // (T*top_k) slot -> padded row, < 0 for a dropped slot
+  const int32_t* ids;     // (T*top_k) expert of each slot
+  const float* tw;        // (T*top_k) routing weights
+  int top_k;
+  int E;
+  const uint4* wt;        // W4 tiles of every expert
+  int64_t w_expert_tiles;
+  const void* scales;
+  int64_t s_expert_stride;
+  const int32_t* zeros;   // AWQ zero words (E, K/g, N/8), the NVFP4 global (E, N), or null
+  int64_t z_expert_stride;
+  int group;
+  int N, K, KT;
+  int tpw;                // K tiles per run of the grouped gemm2's split
+  void* out;
+  int out_dtype;
+  int64_t ldo;
+};
+
+constexpr int kG2cMaxSlots = 16;
+
+// MODE: kModeI4 (int4, group a multiple of 128), kModeE8M0 (MXFP4), kModeNV (NVFP4). SYM: int4
+// without zero points. KTMAX: most K tiles (weights of every tile are loaded up front).
+template <int MODE, bool SYM, int KTMAX>
+__global__ void __launch_bounds__(kG2cMaxSlots * 64) moe_gemm2_combine_kernel(const G2CArgs p) {
+  extern __shared__ __align__(16) unsigned char arows[];  // per wave: KT*128 fp8 codes + 16 bytes
+  __shared__ float ys[kG2cMaxSlots][kTileN];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // top-k slot j
+  const int strip = blockIdx.x;
+  const int64_t t = blockIdx.y;
+  const int64_t slot = t * p.top_k + wave;
+  const int pos = p.inv_pos[slot];
+  const int e = p.ids[slot];
+  const bool valid = pos >= 0 && e >= 0 && e < p.E;  // uniform across the wave
+  const int N = p.N, K = p.K, KT = p.KT;
+  const int astride = KT * kTileK + 16;
+  unsigned char* arow = arows + wave * astride;
+  const int n = strip * kTileN + (lane & 15);  // this lane's output channel
+  float yv = 0.f;
+
+  if (valid) {
+    // ---- weight tiles, scales and zero words of every K tile, issued first
+    const uint4* wt = p.wt + (size_t)((int64_t)e * p.w_expert_tiles) * 64;
+    const int kEsz = MODE == kModeI4 ? 2 : 1;
+    const void* scales = reinterpret_cast<const char*>(p.scales) + (size_t)((int64_t)e * p.s_expert_stride) * kEsz;
+    const int32_t* zeros = p.zeros ? p.zeros + (int64_t)e * p.z_expert_stride : nullptr;
+    const BufRsrc rs_w = make_rsrc(wt, (uint32_t)((N / kTileN) * KT * kTileBytes));
+    const int ngroups = K >> (31 - __builtin_clz((unsigned)p.group));
+    const BufRsrc rs_s = make_rsrc(scales, (uint32_t)(ngroups * N * kEsz));
+    const BufRsrc rs_z = make_rsrc(zeros, (MODE == kModeI4 && zeros) ? (uint32_t)(ngroups * (N / 8) * 4) : 0u);
+    const int gshift = 31 - __builtin_clz((unsigned)(p.group >= kTileK ? p.group / kTileK : 1));
+    uint4 raw[KTMAX];
+    uint16_t sc[KTMAX];
+    uint32_t zw[(MODE == kModeI4 && !SYM) ? KTMAX : 1];
+    int sb[MODE == kModeE8M0 ? KTMAX : 1];
+    uint8_t nvs[MODE == kModeNV ? KTMAX : 1][8];
+#pragma unroll
+    for (int kt = 0; kt < KTMAX; ++kt) {
+      if (kt < KT) {
+        raw[kt] = bload128_nt(rs_w, (uint32_t)lane * 16, (uint32_t)((strip * KT + kt) * kTileBytes));
+        if (MODE == kModeI4) {
+          const int g = kt >> gshift;
+          sc[kt] = bload16(rs_s, (uint32_t)n * 2, (uint32_t)(g * N * 2));
+          if (!SYM) zw[(MODE == kModeI4 && !SYM) ? kt : 0] = bload32(rs_z, (uint32_t)(n / 8) * 4, (uint32_t)(g * (N / 8) * 4));
+        } else if (MODE == kModeE8M0) {
+          sb[MODE == kModeE8M0 ? kt : 0] = (int)bload8(rs_s, (uint32_t)((lane >> 4) * N + n), (uint32_t)(kt * 4 * N));
+        } else {
+#pragma unroll
+          for (int ss = 0; ss < 8; ++ss)
+            nvs[MODE == kModeNV ? kt : 0][ss] = bload8(rs_s, (uint32_t)n, (uint32_t)((kt * 8 + ss) * N));
+        }
+      }
+    }
+
+    // ---- the slot's gemm1 row: per-row fp8 quant into this wave's LDS row (act_quant.h's
+    // arithmetic: s = max(amax / 448, 1e-8), codes = e4m3(x * (1 / s)), the max being exact)
+    constexpr int kAch = (KTMAX * kTileK / 8 + 63) / 64;  // 16-byte loads per lane
+    const uint16_t* src = p.a + (int64_t)pos * p.lda;
+    const int nch = K / 8;
+    uint4 xa[kAch];
+#pragma unroll
+    for (int i = 0; i < kAch; ++i) {
+      const int c = lane + 64 * i;
+      xa[i] = c < nch ? *reinterpret_cast<const uint4*>(src + c * 8) : make_uint4(0u, 0u, 0u, 0u);
+    }
+    float am = 0.f;
+#pragma unroll
+    for (int i = 0; i < kAch; ++i) am = fmaxf(am, amax8(xa[i], p.adtype));
+    const float s = act_row_scale(wave_max(am));
+    const float inv = 1.0f / s;
+#pragma unroll
+    for (int i = 0; i < kAch; ++i) {
+      const int c = lane + 64 * i;
+      if (c < nch) {
+        float f[8];
+        unpack8(xa[i], p.adtype, f);
+        *reinterpret_cast<uint2*>(arow + c * 8) = quant8(f, inv);
+      }
+    }
+    // the row is read back by other lanes of this wave only: LDS serves one wave's accesses in
+    // order, so waiting for the writes (and keeping the compiler from moving the reads above them)
+    // is all the ordering needed -- no workgroup barrier, which waves on dropped slots never reach
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+
+    // ---- K loop: A row 0 of the MFMA is the slot's row (the other rows are zero and unused)
+    const v4f zero4 = v4f{0.f, 0.f, 0.f, 0.f};
+    v4f acc = zero4, tot = zero4;
+    const bool arow_lane = (lane & 15) == 0;
+#pragma unroll
+    for (int kt = 0; kt < KTMAX; ++kt) {
+      if (kt < KT) {
+        v8i at;
+        uint4 lo = make_uint4(0u, 0u, 0u, 0u), hi = lo;
+        if (arow_lane) {
+          const unsigned char* ap = arow + kt * kTileK + 16 * (lane >> 4);
+          lo = *reinterpret_cast<const uint4*>(ap);
+          hi = *reinterpret_cast<const uint4*>(ap + 64);
+        }
+        at[0] = (int)lo.x; at[1] = (int)lo.y; at[2] = (int)lo.z; at[3] = (int)lo.w;
+        at[4] = (int)hi.x; at[5] = (int)hi.y; at[6] = (int)hi.z; at[7] = (int)hi.w;
+        if (MODE == kModeE8M0) {
+          acc = mfma_f8f4_sb(at, fp4_operand(raw[kt]), acc, sb[MODE == kModeE8M0 ? kt : 0]);
+        } else if (MODE == kModeI4 && SYM) {
+          const v4f seed = mfma_f8f8(at, splat8(0xB0B0B0B0u), zero4);  // -R/2
+          const v4f c = mfma_f8f8(at, unpack_tile_int4(raw[kt]), seed);
+          const float scf = f16_to_f32(sc[kt]);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[r] = fmaf(scf, c[r], acc[r]);
+        } else if (MODE == kModeI4) {
+          const v4f rh = mfma_f8f8(at, splat8(kE4M3Half4), zero4);
+          const v4f c = mfma_f8f8(at, unpack_tile_int4(raw[kt]), zero4);
+          const uint32_t z = zw[(MODE == kModeI4 && !SYM) ? kt : 0];
+          const float coef = 15.0f - 2.0f * (float)((z >> (4 * (n & 7))) & 15u);
+          const float scf = f16_to_f32(sc[kt]);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[r] = fmaf(scf, fmaf(coef, rh[r], c[r]), acc[r]);
+        } else {
+          const v8i b = fp4_operand(raw[kt]);
+#pragma unroll
+          for (int ss = 0; ss < 8; ++ss) {
+            const v4f c = mfma_f8f4_sb(at, fp4_half_operand(b, ss), zero4, subgroup_mask_scale(lane, 8, ss));
+            const float scf = __builtin_amdgcn_cvt_f32_fp8((int)(uint32_t)nvs[MODE == kModeNV ? kt : 0][ss], 0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[r] = fmaf(scf, c[r], acc[r]);
+          }
+        }
+        // end of a run of the grouped gemm2's split: fold it into the total in run order
+        if ((kt + 1) % p.tpw == 0 || kt + 1 == KT) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) tot[r] = tot[r] + acc[r];
+          acc = zero4;
+        }
+      }
+    }
+    // row 0 of the C fragment: element 0 of lanes 0..15 (column = lane)
+    float v = tot[0];
+    if (MODE == kModeNV) v *= __int_as_float(zeros[n]);  // the per-output-channel global
+    yv = v * s;
+  }
+  if (lane < kTileN) ys[wave][lane] = yv;
+  __syncthreads();
+  if (threadIdx.x < kTileN) {
+    float acc = 0.f;
+    for (int j = 0; j < p.top_k; ++j) {
+      const int64_t sl = t * p.top_k + j;
+      if (p.inv_pos[sl] >= 0) acc = fmaf(p.tw[sl], ys[j][threadIdx.x], acc);
+    }
+    const int64_t col = (int64_t)strip * kTileN + threadIdx.x;
+    if (p.out_dtype == kF32)
+      reinterpret_cast<float*>(p.out)[t * p.ldo + col] = acc;
+    else
+      reinterpret_cast<uint16_t*>(p.out)[t * p.ldo + col] = to_dtype(acc, p.out_dtype);
+  }
+}
+
+// True when the fused kernel serves these weights: int4 with groups of 128 or more, MXFP4 (E8M0)
+// or NVFP4, K a multiple of 128 up to 2048, top_k up to 16.
+bool moe_gemm2_combine_fits(int64_t K, int scale_fmt, bool has_zeros, int wfmt, int64_t group, int top_k) {
+  const bool fmt = (wfmt == kInt4 && scale_fmt == kScaleF16 && group % kTileK == 0) ||
+                   (wfmt == kE2M1 && scale_fmt == kScaleE8M0 && !has_zeros && group == 32) ||
+                   (wfmt == kE2M1 && scale_fmt == kScaleE4M3 && has_zeros && group == 16);
+  return fmt && K % kTileK == 0 && K <= 16 * kTileK && top_k >= 1 && top_k <= kG2cMaxSlots;
+}
+
+template <int MODE, bool SYM>
+static void g2c_launch(const G2CArgs& a, dim3 grid, dim3 block, size_t lds, hipStream_t st) {
+  if (a.KT <= 8)
+    hipLaunchKernelGGL((moe_gemm2_combine_kernel<MODE, SYM, 8>), grid, block, lds, st, a);
+  else
+    hipLaunchKernelGGL((moe_gemm2_combine_kernel<MODE, SYM, 16>), grid, block, lds, st, a);
+}
+
+// p: the grouped gemm2's arguments as w4a8_moe_gemm would build them for the decode arm (for the
+// K split); the rest is the fused kernel's. The caller checked moe_gemm2_combine_fits.
+int launch_moe_gemm2_combine(const GemmArgs& p, int64_t row_blocks, const uint16_t* a, int64_t lda, int adtype,
+                             const int32_t* inv_pos, const int32_t* ids, const float* tw, int64_t T, int E,
+                             hipStream_t stream) {
+  int waves = 0, tpw = 0;
+  gemv_ksplit(p, row_blocks, waves, tpw);
+  G2CArgs g = {};
+  g.a = a; g.lda = lda; g.adtype = adtype;
+  g.inv_pos = inv_pos; g.ids = ids; g.tw = tw; g.top_k = p.top_k; g.E = E;
+  g.wt = p.wt; g.w_expert_tiles = p.w_expert_tiles;
+  g.scales = p.scales; g.s_expert_stride = p.s_expert_stride;
+  g.zeros = p.zeros; g.z_expert_stride = p.z_expert_stride;
+  g.group = p.group; g.N = (int)p.N; g.K = (int)p.K; g.KT = (int)p.KT; g.tpw = tpw;
+  g.out = p.out; g.out_dtype = p.out_dtype; g.ldo = p.ldo;
+  const dim3 grid((unsigned)(p.N / kTileN), (unsigned)T);
+  const dim3 block((unsigned)(p.top_k * 64));
+  const size_t lds = (size_t)p.top_k * (p.KT * kTileK + 16);
+  if (p.wfmt == kE2M1 && p.sfmt == kScaleE8M0) g2c_launch<kModeE8M0, false>(g, grid, block, lds, stream);
+  else if (p.wfmt == kE2M1) g2c_launch<kModeNV, false>(g, grid, block, lds, stream);
+  else if (p.zeros == nullptr) g2c_launch<kModeI4, true>(g, grid, block, lds, stream);
+  else g2c_launch<kModeI4, false>(g, grid, block, lds, stream);
+  return hipGetLastError() == hipSuccess ? kOk : kErrHip;
+}
+
+}  // namespace w4a8

@@ -42,6 +42,14 @@ _MOE_WMMA_DIM = 16
 _MOE_BLOCK_M_CHOICES = (16, 32, 64, 128)
 # routed rows per expert up to which w4a8_moe runs the skinny grouped GEMV (block_m 16)
 _MOE_SKINNY_MAX_ROWS = 40
+# gemm2 + top-k combine as one launch on the decode arm (python/minisgl/quant/kernels.py:831-850)
+# up to _MOE_G2C_MAX_TOKENS tokens; MINISGL_MOE_G2FUSE=0 keeps the unfused path (requant, gemm2
+# into (P, H) f32, combine), which gives the same bits. The fused kernel reads each routed expert's
+# weights once per token where the grouped gemm2 reads them once per expert; measured on MI355X at
+# configs[4] (whole w4a8_moe call, fused / unfused, us): T=1 25.2/29.5, 2 28.7/33.8, 4 34.0/39.0,
+# 8 47.6/50.3, 12 60.7/59.9, 16 75.4/68.9 -- so up to 8 tokens.
+_MOE_G2FUSE = os.environ.get("MINISGL_MOE_G2FUSE", "1") != "0"
+_MOE_G2C_MAX_TOKENS = 8
 
 
 # --------------------------------------------------------------------------------------------
@@ -609,6 +617,20 @@ def _check_moe_scale_pair(w: torch.Tensor, scales: torch.Tensor, zeros: "torch.T
         )
 
 
+def _moe_gemm2_combine(buf2, topk_ids, tw, inv, T, top_k, bm, P, tiles, E, H, inter, scales, sfmt, zeros, wfmt,
+                       group, out):
+    """gemm2 (per-row requant of the gemm1 buffer in the prologue) + top-k weighted combine as one
+    launch: fp8_wmma.mmq_fp8_moe_gemm2_gather_reduce (python/minisgl/quant/kernels.py:831-850)."""
+    lib = _abi.load()
+    _abi.check(
+        lib.w4a8_moe_gemm2_combine(_abi.ptr(buf2), _abi.dtype_code(buf2.dtype), buf2.stride(0), _abi.ptr(topk_ids),
+                                   _abi.ptr(tw), _abi.ptr(inv), T, top_k, bm, P, _abi.ptr(tiles), E, H, inter,
+                                   _abi.ptr(scales), sfmt, _abi.ptr(zeros), wfmt, group, _abi.ptr(out),
+                                   _abi.dtype_code(out.dtype), out.stride(0), _abi.stream_of(buf2)),
+        "w4a8_moe gemm2+combine",
+    )
+
+
 def _moe_gemm(a, lda, a_scales, a_by_token, sorted_ids, expert_ids, ntp, numel, top_k, bm, P, tiles, E, N, K,
               scales, sfmt, zeros, wfmt, group, out, out_dtype, ldo, silu, arm, what):
     lib = _abi.load()
@@ -726,10 +748,24 @@ def _moe_forward(x, w13, w13_scales, w13_zeros, w2, w2_scales, w2_zeros, gating_
               w13_scales.contiguous(), s13f, w13_zeros.contiguous() if w13_zeros is not None else None, wfmt, _grp,
               buf2, _abi.dtype_code(x.dtype), inter, True, arm, "w4a8_moe gemm1")
 
+    lib = _abi.load()
+    w2s = w2_scales.contiguous()
+    w2z = w2_zeros.contiguous() if w2_zeros is not None else None
+    fuse2 = (_MOE_G2FUSE and arm == _abi.KERNEL_DECODE and M <= _MOE_G2C_MAX_TOKENS
+             and lib.w4a8_moe_gemm2_combine_supported(inter, s2f, int(w2_zeros is not None), wfmt, _grp2, top_k) == 1)
+    if fuse2:
+        # one launch: requant of the gemm1 rows, gemm2, top-k weighted combine (slot order)
+        out = torch.empty((M, K), dtype=x.dtype, device=x.device)
+        engaged(f"w4a8_mi355x.moe_gemm2_combine({arm_name}{e2})")
+        _moe_gemm2_combine(buf2, topk_ids, topk_weights, inv, M, top_k, block_m, P, t2, E, K, inter, w2s, s2f, w2z,
+                           wfmt, _grp2, out)
+        return {"out": out, "buf2": buf2, "y2": None, "topk_weights": topk_weights, "topk_ids": topk_ids,
+                "sorted_ids": sorted_ids, "expert_ids": expert_ids, "ntp": ntp, "inv_pos": inv, "block_m": block_m,
+                "fused_gemm2": True}
+
     # gemm2 input: per-row fp8 re-quant of the (P, inter) buffer, rows bounded by ntp on device
     q2 = torch.empty((P, inter), dtype=torch.uint8, device=x.device)
     s2 = torch.empty((P,), dtype=torch.float32, device=x.device)
-    lib = _abi.load()
     # rows that can hold data: every expert with slots pads to whole blocks, so ntp <= this bound;
     # the kernel reads ntp on the device and skips the rest, the bound only sizes the grid
     rows = min(P, (numel // block_m + min(E, numel)) * block_m)
@@ -738,11 +774,11 @@ def _moe_forward(x, w13, w13_scales, w13_zeros, w2, w2_scales, w2_zeros, gating_
     y2 = torch.empty((P, K), dtype=torch.float32, device=x.device)
     engaged(f"w4a8_mi355x.moe_gemm2({arm_name}{e2})")
     _moe_gemm(q2, inter, s2, 0, sorted_ids, expert_ids, ntp, numel, top_k, block_m, P, t2, E, K, inter,
-              w2_scales.contiguous(), s2f, w2_zeros.contiguous() if w2_zeros is not None else None, wfmt, _grp2,
-              y2, _abi.F32, K, False, arm, "w4a8_moe gemm2")
+              w2s, s2f, w2z, wfmt, _grp2, y2, _abi.F32, K, False, arm, "w4a8_moe gemm2")
     out = torch.empty((M, K), dtype=x.dtype, device=x.device)
     engaged("w4a8_mi355x.moe_combine")
     _abi.check(lib.w4a8_moe_combine(_abi.ptr(y2), K, _abi.ptr(inv), _abi.ptr(topk_weights), M, top_k, K,
                                     _abi.ptr(out), _abi.dtype_code(x.dtype), _abi.stream_of(x)), "w4a8_moe combine")
     return {"out": out, "buf2": buf2, "y2": y2, "topk_weights": topk_weights, "topk_ids": topk_ids,
-            "sorted_ids": sorted_ids, "expert_ids": expert_ids, "ntp": ntp, "inv_pos": inv, "block_m": block_m}
+            "sorted_ids": sorted_ids, "expert_ids": expert_ids, "ntp": ntp, "inv_pos": inv, "block_m": block_m,
+            "fused_gemm2": False}

@@ -1,9 +1,12 @@
 """GPU parity of the dense W4A8 path against the CPU oracle (all through the C ABI).
 
 Bars: fp8 activation codes and scales bit-exact; GEMM outputs within 2e-3 relative L2 of the
-oracle's f64 result, with an element-wise structural guard (see assert_close_to_oracle). Full BASELINE sizes are checked against the oracle where it finishes in
-seconds (every decode shape), and through row subsets plus bit-exact row-split invariance for the
-prefill shapes.
+oracle's f64 result (the contract), within 5e-4 relative L2 of that result rounded to the output
+dtype (what f32 accumulation leaves: see assert_close_to_oracle), with an element-wise structural
+guard. Full BASELINE sizes are checked against the oracle where it finishes in seconds (every
+decode shape), and through row subsets plus bit-exact row-split invariance for the prefill shapes.
+The decode arm is checked for M-invariance: rows[0:m] alone equal the same rows inside a 16-row
+call, bit for bit.
 """
 import numpy as np
 import pytest
@@ -15,6 +18,13 @@ from conftest import pkg
 pytestmark = pytest.mark.gpu
 
 REL_L2 = 2e-3
+# Against the oracle rounded to the output dtype, an output differs only where the kernel's f32
+# accumulation error moves a value across a rounding boundary of the output dtype. With the
+# accumulation error e (relative, about 2^-24 * sqrt(K) for sums of K random-sign terms: under
+# 1e-5 at K <= 28672) such a crossing has probability about 2e / ulp and costs one ulp, so the
+# relative L2 is about sqrt(2e / ulp) * ulp: 2.5e-4 for bf16 (ulp 2^-8) and 1e-4 for fp16 at the
+# largest K. The bar leaves 2x over the bf16 figure.
+REL_L2_ROUNDED = 5e-4
 
 
 def _sync():
@@ -22,7 +32,8 @@ def _sync():
 
 
 def assert_close_to_oracle(got: torch.Tensor, ref: np.ndarray, what: str):
-    """Contract bar: rel L2 <= 2e-3 against the f64 oracle. Structural guard: every element within
+    """Contract bar: rel L2 <= 2e-3 against the f64 oracle. Kernel bar: rel L2 <= 5e-4 against the
+    oracle rounded to the output dtype (REL_L2_ROUNDED). Structural guard: every element within
     two output-dtype ulps plus 1e-4 of the output's magnitude (the MFMA's fp8 dot product
     accumulates with slightly less than f32 precision, ~1e-5 relative, which shows up only where
     outputs are small through cancellation)."""
@@ -37,6 +48,7 @@ def assert_close_to_oracle(got: torch.Tensor, ref: np.ndarray, what: str):
     print(f"[parity] {what}: rel L2 {rel:.3e} (vs dtype-rounded oracle {rel_r:.3e}), outliers {int(bad.sum())}",
           flush=True)
     assert rel <= REL_L2, f"{what}: rel L2 {rel:.3e} > {REL_L2}"
+    assert rel_r <= REL_L2_ROUNDED, f"{what}: rel L2 vs the dtype-rounded oracle {rel_r:.3e} > {REL_L2_ROUNDED}"
     assert not bad.any(), f"{what}: {bad.sum()} elements off, worst {np.abs(g - ref)[bad].max():.3e}"
     return rel
 
@@ -109,6 +121,37 @@ def test_config2_decode_sweep(kernels, oracle, dev, K, N):
         out = kernels.w4a8_linear(xd[:M].contiguous(), tiles, sd, None, g)
         _sync()
         assert_close_to_oracle(out, ref[:M], f"K={K} N={N} M={M}")
+
+
+M_INV_CASES = [(4096, 6144, 128, "sym"), (4096, 4096, 128, "sym"), (4096, 28672, 128, "sym"), (14336, 4096, 128, "sym"),
+               (2560, 9728, 128, "asym"), (2048, 9600, 128, "sym"), (1536, 768, 32, "asym"), (4096, 8192, 32, "e2m1")]
+
+
+@pytest.mark.parametrize("K,N,g,fmt", M_INV_CASES)
+def test_decode_m_invariance(kernels, dev, K, N, g, fmt):
+    """The decode arm's self-invariance (tools/quant_m_invariance.py:119-130; the reference records
+    worst max|delta| = 0 in _qminv_dense.txt:30-33): rows[0:m] computed alone equal rows[0:m] inside
+    a 16-row call, bit for bit, for m = 1..16 -- the Llama-3-8B shapes, configs[0], a 600-strip
+    weight whose two-strip grid is small, a sub-tile group and MXFP4. The fused silu arm is held to
+    the same."""
+    x = synth.activations(16, K, seed=K + N + g, outliers=True).to(dev)
+    if fmt == "e2m1":
+        w, s = synth.mxfp4_weight(N, K, seed=N + 3)
+        z = None
+    else:
+        w, s, z = synth.int4_weight(N, K, g, seed=N + 3, asym=fmt == "asym", scale_floor=1e-4)
+    e2 = fmt == "e2m1"
+    tiles = kernels.repack_w4(w.to(dev), weight_is_e2m1=e2)
+    sd, zd = s.to(dev), None if z is None else z.to(dev)
+    full = kernels.w4a8_linear(x, tiles, sd, zd, g, kernel="decode_gemv", weight_is_e2m1=e2)
+    fsilu = kernels.w4a8_linear_silu(x, tiles, sd, zd, g, weight_is_e2m1=e2)
+    for m in range(1, 17):
+        part = kernels.w4a8_linear(x[:m].contiguous(), tiles, sd, zd, g, kernel="decode_gemv", weight_is_e2m1=e2)
+        psilu = kernels.w4a8_linear_silu(x[:m].contiguous(), tiles, sd, zd, g, weight_is_e2m1=e2)
+        _sync()
+        d = (part.float() - full[:m].float()).abs().max().item()
+        assert torch.equal(part, full[:m]), f"K={K} N={N} g={g} {fmt}: rows[0:{m}] differ, max|d| {d:.3e}"
+        assert torch.equal(psilu, fsilu[:m]), f"K={K} N={N} g={g} {fmt}: silu rows[0:{m}] differ"
 
 
 def test_decode_accepts_op_layout_and_explicit_zeros(kernels, oracle, dev):
