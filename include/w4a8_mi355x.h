@@ -94,6 +94,19 @@ int w4a8_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, c
                 int out_dtype, int64_t ldo, int silu, void* workspace, int64_t workspace_bytes, int kernel,
                 void* stream);
 
+/* w4a8_linear for callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). No counterpart in the reference: its ops
+ * allocate their act-quant buffers in-op. Same arguments and results as w4a8_linear, bit for bit,
+ * minus the workspace: the act-quant staging (w4a8_linear_workspace_bytes(M, K)) lives in a static
+ * device array of w4a8_linear_noalloc_max_bytes() = 64 MiB that each GPU holds from its first call
+ * until the process ends. Larger M*K is refused (kErrInvalid, message names the limit). Calls on
+ * one GPU share that array, so calls that overlap on one GPU (several streams or threads) race.
+ * The entry point calls no allocator. */
+int64_t w4a8_linear_noalloc_max_bytes(void);
+int w4a8_linear_noalloc(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const void* w_tile, int64_t N,
+                        const void* scales, int scale_fmt, const int32_t* zeros, int wfmt, int64_t group_size,
+                        void* out, int out_dtype, int64_t ldo, int silu, int kernel, void* stream);
+
 /* Softmax + top-k (ties keep the lower expert index) + optional renormalisation. Replaces the
  * route half of moe_hip.moe_route_align (python/minisgl/quant/kernels.py:423-447; tie rule
  * python/minisgl/layers/moe.py:1218-1227). E <= 512. */

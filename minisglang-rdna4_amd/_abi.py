@@ -35,6 +35,9 @@ SIGNATURES = {
     "w4a8_linear_workspace_bytes": (_c_i64, [_c_i64, _c_i64]),
     "w4a8_linear": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _c_i64, _vp, _c_i64, _vp, _c_int, _vp, _c_int, _c_i64,
                              _vp, _c_int, _c_i64, _c_int, _vp, _c_i64, _c_int, _vp]),
+    "w4a8_linear_noalloc_max_bytes": (_c_i64, []),
+    "w4a8_linear_noalloc": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _c_i64, _vp, _c_i64, _vp, _c_int, _vp, _c_int,
+                                     _c_i64, _vp, _c_int, _c_i64, _c_int, _c_int, _vp]),
     "w4a8_moe_route": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _c_int, _c_int, _vp, _vp, _vp]),
     "w4a8_rms_norm": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _c_i64, _vp, _c_i64, _vp, _c_int, ctypes.c_float, _vp,
                                _c_i64, _vp, _c_i64, _vp, _vp]),
