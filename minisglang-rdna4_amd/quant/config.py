@@ -12,9 +12,14 @@ predicates, the module filter (is_module_quantized, for_module) and QuantConfig.
     format "mixed-precision") are all kept, class-name targets ("Linear") treated as catch-alls
     and ordered last, and for_module picks the first group whose targets match;
   * modelopt (NVFP4 / FP8 headers) is rewritten into the compressed-tensors shape first, glob
-    ignore entries becoming anchored regexes.
-Other methods (including AMD Quark headers) give None: the checkpoint is not one these kernels
-serve.
+    ignore entries becoming anchored regexes;
+  * AMD Quark (config.py:228-293, called at :515) is rewritten the same way: the weight format is
+    the (dtype, scale_format) pair of global_quant_config.weight, looked up in a closed table, and
+    `exclude` names parameter tensors, so their `.weight` / `.bias` / `.weight_scale` suffix is cut
+    to the module name the ignore match uses. Dynamic weight quant, per-layer override tables and
+    any on-disk packing other than "reorder" are refused (None): each would load without error and
+    compute wrong numbers.
+Other methods give None: the checkpoint is not one these kernels serve.
 """
 from __future__ import annotations
 
@@ -77,6 +82,47 @@ def _modelopt_to_ct(d: dict) -> dict | None:
         groups = {k: dict(g, targets=tuple(tgt(t) for t in (g.get("targets") or ()))) for k, g in groups.items()}
     return {"quant_method": "compressed-tensors", "format": fmt, "config_groups": groups,
             "ignore": tuple(_glob_to_ignore(p) for p in _norm_ignore(d.get("ignore") or ()))}
+
+
+# Quark weight (dtype, scale_format) -> the compressed-tensors format with the same on-disk layout.
+# Closed: a pair not listed is a packing no reader here understands, and is refused.
+_QUARK_FORMAT = {
+    ("fp4", "e8m0"): "mxfp4-pack-quantized",   # E2M1 codes, E8M0 block exponents
+    ("fp4", "e4m3"): "nvfp4-pack-quantized",   # E2M1 codes, e4m3 block scales, per-tensor global
+    ("fp8_e4m3", "float"): "float-quantized",
+    ("fp8_e4m3", ""): "float-quantized",
+}
+_QUARK_PACKINGS = ("reorder",)  # the nibble order the compressed-tensors readers expect
+_PARAM_SUFFIXES = (".weight", ".bias", ".weight_scale")
+
+
+def _strip_param_suffix(name: str) -> str:
+    for sfx in _PARAM_SUFFIXES:
+        if name.endswith(sfx):
+            return name[: -len(sfx)]
+    return name
+
+
+def _quark_to_ct(d: dict) -> dict | None:
+    """Quark header -> compressed-tensors shape (config.py:228-293), None when it is refused."""
+    gq = d.get("global_quant_config") or {}
+    w = gq.get("weight") or gq.get("weights") or {}
+    dt = str(w.get("dtype") or "").lower()
+    fmt = _QUARK_FORMAT.get((dt, str(w.get("scale_format") or "").lower()))
+    if fmt is None or w.get("is_dynamic"):
+        return None
+    if d.get("layer_quant_config") or d.get("layer_type_quant_config"):
+        return None  # per-layer overrides: no reader for a per-layer mixed scheme
+    packing = str((d.get("export") or {}).get("pack_method") or "reorder").lower()
+    if packing not in _QUARK_PACKINGS:
+        return None
+    weights = {"num_bits": 4 if dt == "fp4" else 8, "type": "float", "strategy": "group",
+               "group_size": int(w.get("group_size") or 32), "symmetric": True}
+    return {"quant_method": "compressed-tensors", "format": fmt,
+            # the checkpoint's activation scheme is not consumed: the methods pick per-token fp8
+            # (W4A8) or unquantized (W4A16), as for a compressed-tensors file declaring none
+            "config_groups": {"group_0": {"targets": ["Linear"], "weights": weights, "input_activations": None}},
+            "ignore": _norm_ignore(_strip_param_suffix(str(e)) for e in (d.get("exclude") or ()))}
 
 
 def _targets(targets) -> tuple[tuple[str, ...], bool]:
@@ -196,6 +242,11 @@ class QuantConfig:
         method = str(d.get("quant_method", "")).lower()
         if method in ("modelopt", "modelopt_fp8", "modelopt_fp4"):
             d = _modelopt_to_ct(d)
+            if d is None:
+                return None
+            method = "compressed-tensors"
+        if method == "quark":
+            d = _quark_to_ct(d)
             if d is None:
                 return None
             method = "compressed-tensors"

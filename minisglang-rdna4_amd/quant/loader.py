@@ -16,7 +16,9 @@ modules:
 NVFP4's per-tensor global arrives under its producer's field name (compressed-tensors
 `weight_global_scale`, a divisor; modelopt `weight_scale_2`, a multiplier) and is normalised by
 quant.nvfp4.split_nvfp4_scale into the per-output-channel vector the method declares as
-`weight_global`; modelopt's packed codes are named `weight`. Activation calibration tensors
+`weight_global`. modelopt and AMD Quark name the packed 4-bit codes `weight` (uint8) where
+compressed-tensors says `weight_packed`; the loader reads either (python/minisgl/models/weight.py:
+1025-1045, which renames on the uint8 dtype the same way). Activation calibration tensors
 (`input_global_scale`, `input_scale`) and compressed-tensors' `weight_shape` are not used.
 """
 from __future__ import annotations
@@ -79,8 +81,9 @@ def _fetch(tensors: dict, prefix: str, attr: str, declared: torch.Tensor, nvfp4:
     if nvfp4 and attr == "weight_global":
         return _nvfp4_global(tensors, prefix)
     key = f"{prefix}.{attr}"
-    if key not in tensors and nvfp4 and attr == "weight_packed" and f"{prefix}.weight" in tensors:
-        key = f"{prefix}.weight"  # modelopt names the packed codes `weight`
+    alt = f"{prefix}.weight"
+    if key not in tensors and attr == "weight_packed" and alt in tensors and tensors[alt].dtype == torch.uint8:
+        key = alt  # modelopt / Quark name the packed codes `weight`; a full-precision weight is never uint8
     if key not in tensors:
         raise KeyError(f"missing checkpoint tensor {key}")
     return tensors[key]

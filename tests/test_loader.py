@@ -186,3 +186,78 @@ def test_gptq_experts_stacked(tmp_path):
         assert torch.equal(w13._zeros_op[e], torch.cat([o[2] for o in ops], dim=1))
         d = K_.gptq_to_op_layout(t[f"x.{e}.down_proj.qweight"], t[f"x.{e}.down_proj.scales"], t[f"x.{e}.down_proj.qzeros"])
         assert torch.equal(w2._scales_op[e], d[1])
+
+
+# ------------------------------------------------------------------------------------ AMD Quark
+def _quark(dtype, sfmt, **extra):
+    w = {"dtype": dtype, "scale_format": sfmt, "group_size": extra.pop("group_size", 32), "is_dynamic": False}
+    w.update(extra.pop("weight_extra", {}))
+    d = {"quant_method": "quark", "global_quant_config": {"weight": w,
+                                                          "input_tensors": {"dtype": "fp4", "is_dynamic": False}},
+         "exclude": ["lm_head", "model.language_model.layers.0.mlp.gate.weight", "mtp.layers.0.mlp.gate_proj.weight",
+                     "model.layers.1.self_attn.q_proj.bias", "model.layers.2.mlp.up_proj.weight_scale"],
+         "export": {"pack_method": "reorder"}}
+    d.update(extra)
+    return {"quantization_config": d}
+
+
+def test_from_hf_quark_formats_and_exclude_suffixes():
+    """Quark (python/minisgl/quant/config.py:228-293): the (dtype, scale_format) pair names the
+    format; exclude entries name tensors, cut to their module (else `mtp...gate_proj.weight` would
+    match no module and the unquantized tensor would load as a quantized layer)."""
+    mx = Q.from_hf(_quark("fp4", "e8m0"))
+    assert mx.is_compressed_tensors and mx.weight_is_e2m1 and not mx.is_nvfp4 and mx.group_size == 32
+    assert mx.ct_format == "mxfp4-pack-quantized" and mx.act_type is None
+    assert mx.ignore == ("lm_head", "model.layers.0.mlp.gate", "mtp.layers.0.mlp.gate_proj",
+                         "model.layers.1.self_attn.q_proj", "model.layers.2.mlp.up_proj")
+    assert mx.for_module("mtp.layers.0.mlp.gate_proj") is None
+    assert mx.for_module("model.layers.0.mlp.gate") is None
+    assert mx.for_module("model.layers.3.mlp.gate_proj") is mx
+    assert isinstance(M_.create_linear_method(mx), M_.MxFp4LinearMethod)
+    nv = Q.from_hf(_quark("fp4", "e4m3", group_size=16))
+    assert nv.is_nvfp4 and nv.group_size == 16 and isinstance(M_.create_linear_method(nv), M_.NvFp4LinearMethod)
+    f8 = Q.from_hf(_quark("fp8_e4m3", "float"))
+    assert f8.is_fp8_w8a8 and f8.ct_format == "float-quantized"
+    assert Q.from_hf(_quark("fp8_e4m3", "")).is_fp8_w8a8
+
+
+@pytest.mark.parametrize("bad", [
+    dict(dtype="int4", sfmt="float"),                          # pair outside the closed table
+    dict(dtype="fp4", sfmt="fp16"),
+    dict(dtype="fp4", sfmt="e8m0", weight_extra={"is_dynamic": True}),
+    dict(dtype="fp4", sfmt="e8m0", layer_quant_config={"model.layers.0.mlp.down_proj": {"weight": {"dtype": "fp8_e4m3"}}}),
+    dict(dtype="fp4", sfmt="e8m0", layer_type_quant_config={"Linear": {}}),
+    dict(dtype="fp4", sfmt="e8m0", export={"pack_method": "order"}),
+])
+def test_from_hf_quark_refusals(bad):
+    """Each refusal returns None (the header is not served) instead of a scheme that would load
+    and compute wrong numbers: dynamic weight quant, per-layer overrides, an unknown packing."""
+    bad = dict(bad)
+    assert Q.from_hf(_quark(bad.pop("dtype"), bad.pop("sfmt"), **bad)) is None
+
+
+def test_quark_mxfp4_layer_from_safetensors(tmp_path):
+    """A Quark MXFP4 checkpoint names the packed codes `weight` (uint8) beside `weight_scale`; the
+    loader builds the same layer as from the compressed-tensors names."""
+    K, I = 256, 32
+    q = Q.from_hf(_quark("fp4", "e8m0"))
+    gen = synth.gen(8)
+    quark, ct = {}, {}
+    for p in ("gate_proj", "up_proj"):
+        codes = torch.randint(0, 256, (I, K // 2), generator=gen, dtype=torch.int32).to(torch.uint8)
+        sc = torch.randint(119, 128, (I, K // 32), generator=gen, dtype=torch.int32).to(torch.uint8)
+        quark[f"model.layers.3.mlp.{p}.weight"] = codes
+        quark[f"model.layers.3.mlp.{p}.weight_scale"] = sc
+        ct[f"model.layers.3.mlp.{p}.weight_packed"] = codes
+        ct[f"model.layers.3.mlp.{p}.weight_scale"] = sc
+    parts = ["model.layers.3.mlp.gate_proj", "model.layers.3.mlp.up_proj"]
+    mq, lq = LD.build_linear(q, "model.layers.3.mlp.gate_up_proj", K, 2 * I, _roundtrip(tmp_path, quark), parts=parts,
+                             device="cpu")
+    mc, lc = LD.build_linear(q, "model.layers.3.mlp.gate_up_proj", K, 2 * I, ct, parts=parts, device="cpu")
+    assert isinstance(mq, M_.MxFp4LinearMethod)
+    dq, dc = LD._declared(lq), LD._declared(lc)
+    assert dq.keys() == dc.keys() and all(torch.equal(dq[k], dc[k]) for k in dq)
+    # a full-precision `weight` is never taken for the packed codes
+    with pytest.raises(KeyError, match="weight_packed"):
+        LD.build_linear(q, "m", K, I, {"m.weight": torch.randn(I, K).to(torch.bfloat16),
+                                       "m.weight_scale": torch.zeros(I, K // 32, dtype=torch.uint8)}, device="cpu")
