@@ -176,7 +176,7 @@ __host__ __device__ inline int stage_stride(int KT) { return KT * kTileK + 16; }
 //        block.
 //   GPT: groups per K tile for the sub-tile-group modes (1 for the others).
 template <int NSTR, int CH, int MODE, int AMODE, bool SYM, int SM, int GPT>
-__global__ void __launch_bounds__(512) gemv_kernel(const GemmArgs p, int tpw) {
+__global__ void __launch_bounds__(512) gemv_kernel(const GemmArgs p, int tpw, int afirst) {
   constexpr int WFMT = (MODE == kModeE8M0 || MODE == kModeE2M1F16 || MODE == kModeNV) ? kE2M1 : kInt4;
   static_assert(MODE != kModeNV || GPT == 8, "NVFP4 tiles hold 8 groups");
   constexpr bool kStaged = AMODE != kAGlobal;
@@ -315,9 +315,11 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemmArgs p, int tpw) {
   // tile index for a slot load; past the range end it repeats the last tile (a cache hit that
   // keeps the loads unconditional)
   auto clamp_kt = [&](int kt) { return kt < kt_end ? kt : (kt_end > 0 ? kt_end - 1 : 0); };
-  // fill the window: the first CH tiles' loads are in flight while A is staged
+  // fill the window: the first CH tiles' loads are in flight while A is staged (afirst: after)
+  if (!(kStaged && afirst)) {
 #pragma unroll
-  for (int t = 0; t < CH; ++t) load_tile(t, clamp_kt(kt_begin + t));
+    for (int t = 0; t < CH; ++t) load_tile(t, clamp_kt(kt_begin + t));
+  }
 
   if (AMODE == kAQuant) {
     // per-row amax: lane r (< 16) of each wave ends with the wave's maximum of row r
@@ -386,6 +388,10 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemmArgs p, int tpw) {
       }
     }
     __syncthreads();
+  }
+  if (kStaged && afirst) {
+#pragma unroll
+    for (int t = 0; t < CH; ++t) load_tile(t, clamp_kt(kt_begin + t));
   }
   const int lrow = kStaged ? ((lane & 15) < rv ? (lane & 15) : 0) : 0;
 
@@ -534,6 +540,7 @@ struct GemvPlan {
   int amode;    // kAGlobal / kAStage / kAQuant
   int sm;       // staging loads per thread (4 or 8) for kAStage / kAQuant
   size_t stage_bytes;  // LDS bytes of the staged A block (0 for kAGlobal)
+  int afirst;          // staged A sources: stage A before issuing any weight load
 };
 
 // Kernel launch of one A source; defined in the unit that instantiates it. `grid` is
@@ -567,21 +574,21 @@ template <int NS, int CHK, int MD, int AM, bool SY>
 void gemv_launch_sm(const GemmArgs& p, dim3 grid, dim3 block, size_t lds, hipStream_t stream, const GemvPlan& pl) {
   constexpr int G = MD == kModeNV ? 8 : 1;
   if constexpr (AM == kAGlobal) {
-    hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 4, G>), grid, block, lds, stream, p, pl.tpw);
+    hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 4, G>), grid, block, lds, stream, p, pl.tpw, pl.afirst);
   } else if constexpr (AM == kAStage) {
     if (pl.sm <= 4)
-      hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 4, G>), grid, block, lds, stream, p, pl.tpw);
+      hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 4, G>), grid, block, lds, stream, p, pl.tpw, pl.afirst);
     else
-      hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 8, G>), grid, block, lds, stream, p, pl.tpw);
+      hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 8, G>), grid, block, lds, stream, p, pl.tpw, pl.afirst);
   } else {
     if (pl.sm == 1)
-      hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 1, G>), grid, block, lds, stream, p, pl.tpw);
+      hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 1, G>), grid, block, lds, stream, p, pl.tpw, pl.afirst);
     else if (pl.sm == 2)
-      hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 2, G>), grid, block, lds, stream, p, pl.tpw);
+      hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 2, G>), grid, block, lds, stream, p, pl.tpw, pl.afirst);
     else if (pl.sm == 4)
-      hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 4, G>), grid, block, lds, stream, p, pl.tpw);
+      hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 4, G>), grid, block, lds, stream, p, pl.tpw, pl.afirst);
     else
-      hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 8, G>), grid, block, lds, stream, p, pl.tpw);
+      hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 8, G>), grid, block, lds, stream, p, pl.tpw, pl.afirst);
   }
 }
 
