@@ -10,8 +10,11 @@ per step) so no step re-reads weights out of the 256 MB Infinity Cache.
 value = algorithmic bytes of the step (codes N*K/2 + fp16 scales + bf16 x in + bf16 out) x steps /
 wall time, with everything resident in HBM. The roofline object is the decode GEMV kernel alone at
 the largest shape (gate_up, M=1, one launch per call): algorithmic bytes per launch / mean launch
-time from HIP events on the launch stream, against 8 TB/s. cpu_baseline is the reference's
-dequantize-then-matmul CPU path (oracle/baseline.py) on a bounded sample, rank 0 only.
+time from HIP events on the launch stream, against 8 TB/s. decode_per_shape times every call of the
+step on its own (GB/s and fraction per shape and M). cpu_baseline is the reference's
+dequantize-then-matmul CPU path (oracle/baseline.py): the whole sweep step on all host cores, median
+of 5 passes, with the CPU model, rank 0 only. prefill_config3 is configs[2]/[3]: every shape at
+M = 512, 2048, 8192 on the producer pair (act-quant outside the timed region).
 
 other_configs reports the remaining BASELINE configs through the same operator API: cfg1 (AWQ
 zero-point int4, M=16, K=2560, N=9728), cfg4 (MoE E=128 top-8 H=2048 I=768, T in {1,16,256,4096})
@@ -26,7 +29,8 @@ producer: once with the linear quantizing its bf16 input, once with the producer
 (no act-quant launches).
 
 Modes for profiling runs (same committed file): --profile-kernel runs only the roofline loop,
---copy-calib runs a plain device copy of known size (for scaling rocprofv3 byte counters).
+--profile-prefill FMT M K N times one prefill GEMM, --copy-calib runs a plain device copy of known
+size (for scaling rocprofv3 byte counters).
 """
 from __future__ import annotations
 
@@ -77,12 +81,16 @@ def make_x(M: int, K: int, seed: int, dev):
 def cpu_baseline_leg() -> dict:
     from oracle import baseline
 
-    r = baseline.run(SHAPES, MS, GROUP, seed=1)
+    r = baseline.run(SHAPES, MS, GROUP, seed=1, repeats=5)
     gbs = r["bytes"] / r["seconds"] / 1e9
     return {"value": round(gbs, 4), "unit": "GB/s", "cores": r["cores"], "kind": "port",
+            "cpu_model": r["cpu_model"],
+            "median_of": r["repeats"], "seconds_per_pass": r["all_seconds"],
+            "dequant_s": round(r["dequant_s"], 4), "matmul_s": round(r["matmul_s"], 4),
+            "total_s": round(r["seconds"], 4),
             "sample": f"one full sweep step (4 Llama-3-8B shapes x M in {{1,2,4,8,16}}), {r['bytes'] / 1e6:.0f} MB "
-                      f"algorithmic; per call: per-token e4m3 round trip + int4 dequant to f32 (total "
-                      f"{r['dequant_s']:.2f} s) + f32 matmul ({r['matmul_s']:.2f} s); torch CPU, {r['cores']} threads"}
+                      f"algorithmic, timed {r['repeats']} times (median pass reported); per call: per-token e4m3 "
+                      f"round trip + int4 dequant to f32 + f32 matmul; torch CPU, {r['cores']} threads"}
 
 
 def roofline_leg(kernels, dev, reps: int = 60) -> dict:
@@ -126,14 +134,16 @@ def roofline_leg(kernels, dev, reps: int = 60) -> dict:
 
 
 def prefill_leg(kernels, dev) -> dict:
-    """TFLOPS of the MFMA GEMM at config-3 shapes (M=2048 and M=8192), one warm + timed calls."""
+    """TFLOPS of the MFMA GEMM at every configs[2]/[3] shape (M = 512, 2048, 8192), one warm call
+    then 5 timed calls on the producer pair (x_fp8, act_scales): the act-quant launch is outside the
+    timed region (in_op_quant_us adds it back for one shape per M)."""
     import torch
 
-    out = {}
+    out = {"input": "producer pair (x_fp8, act_scales); act-quant outside the timed region"}
     gen = torch.Generator(device=dev).manual_seed(9)
     for K, N in SHAPES:
         tiles, sc = make_weights(kernels, K, N, gen, dev)
-        for M in (2048, 8192):
+        for M in (512, 2048, 8192):
             x = make_x(M, K, 90 + M, dev)
             q, s = kernels.act_quant(x)
             kernels.w4a8_linear(x, tiles, sc, None, GROUP, x_fp8=q, act_scales=s)
@@ -149,8 +159,52 @@ def prefill_leg(kernels, dev) -> dict:
             tflops = 2.0 * M * N * K / (us * 1e-6) / 1e12
             out[f"{K}x{N}_M{M}"] = {"us": round(us, 1), "tflops": round(tflops, 1),
                                     "frac_fp8_peak": round(tflops / FP8_PEAK_TFLOPS, 4)}
+            if (K, N) == (4096, 28672):
+                out[f"{K}x{N}_M{M}"]["in_op_quant_us"] = round(
+                    _time_calls([lambda: kernels.w4a8_linear(x, tiles, sc, None, GROUP)], 5), 1)
         del tiles, sc
     return out
+
+
+def decode_shapes_leg(kernels, dev) -> dict:
+    """Every configs[1] call on its own: (shape, M) -> mean us per call (act-quant + GEMV, or the
+    one fused launch) with back-to-back launches, weights rotated over more than 600 MB (over twice
+    the MALL) so every call streams from HBM; GB/s on the algorithmic bytes and the fraction of the
+    8 TB/s peak."""
+    import torch
+
+    out = {}
+    gen = torch.Generator(device=dev).manual_seed(5)
+    for K, N in SHAPES:
+        wbytes = N * K // 2 + (K // GROUP) * N * 2
+        copies = [make_weights(kernels, K, N, gen, dev) for _ in range(max(4, (600 << 20) // wbytes + 1))]
+        for M in MS:
+            x = make_x(M, K, 100 + M, dev)
+            us = _time_calls([lambda c=c: kernels.w4a8_linear(x, c[0], c[1], None, GROUP) for c in copies],
+                             max(60, 2 * len(copies)))
+            out[f"{K}x{N}_M{M}"] = _gbs(algo_bytes(M, K, N), us)
+        del copies
+        torch.cuda.empty_cache()
+    return out
+
+
+def profile_prefill(kernels, dev, fmt: str, M: int, K: int, N: int) -> dict:
+    """One prefill GEMM shape, 2 warm + 5 timed calls on the producer pair, for counter runs."""
+    import torch
+
+    gen = torch.Generator(device=dev).manual_seed(9)
+    if fmt == "int4":
+        tiles, sc = make_weights(kernels, K, N, gen, dev)
+        g, e2 = GROUP, False
+    else:
+        tiles = kernels.repack_w4(_rand_words((N, K // 8), gen, dev), weight_is_e2m1=True)
+        sc = torch.randint(119, 128, (K // 32, N), generator=gen, device=dev, dtype=torch.int32).to(torch.uint8)
+        g, e2 = 32, True
+    x = make_x(M, K, 5, dev)
+    q, s = kernels.act_quant(x)
+    us = _time_calls([lambda: kernels.w4a8_linear(x, tiles, sc, None, g, weight_is_e2m1=e2, x_fp8=q,
+                                                  act_scales=s)], 5)
+    return {"profile_prefill": fmt, "M": M, "K": K, "N": N, **_tflops(2.0 * M * N * K, us)}
 
 
 def _time_calls(calls, reps: int) -> float:
@@ -377,6 +431,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-configs", action="store_true")
+    ap.add_argument("--profile-prefill", nargs=4, metavar=("FMT", "M", "K", "N"),
+                    help="time one prefill GEMM (FMT int4 or mxfp4) and exit, for counter runs")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -404,6 +460,10 @@ def main() -> int:
     if args.profile_kernel:
         r = roofline_leg(kernels, dev)
         print(json.dumps(r))
+        return 0
+    if args.profile_prefill:
+        f, m, k, n = args.profile_prefill
+        print(json.dumps(profile_prefill(kernels, dev, f, int(m), int(k), int(n))))
         return 0
 
     # ---- sweep setup: 5 weight copies (one per M), activations per (M, shape)
@@ -448,6 +508,7 @@ def main() -> int:
     # per-shape GEMV-only view (events around graph replays of one call each would add a graph per
     # shape; the roofline leg covers the dominant shape)
     roof = roofline_leg(kernels, dev)
+    per_shape = decode_shapes_leg(kernels, dev)
     prefill = None if args.no_prefill else prefill_leg(kernels, dev)
     others = None if args.no_configs else configs_leg(kernels, dev)
     producer = None if args.no_configs else producer_leg(kernels, dev, weights)
@@ -480,6 +541,7 @@ def main() -> int:
         },
         "roofline": roof,
         "cpu_baseline": cpu,
+        "decode_per_shape": per_shape,
         "prefill_config3": prefill,
         "other_configs": others,
         "next_formats": formats,

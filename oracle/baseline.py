@@ -28,29 +28,52 @@ def _dequant_int4(w_packed: torch.Tensor, scales: torch.Tensor, group: int) -> t
     return (q - 8.0) * scales.float().t().repeat_interleave(group, dim=1)
 
 
-def run(shapes, Ms, group: int, seed: int = 0) -> dict:
+def cpu_model() -> str:
+    """The host CPU's model name (lscpu's 'Model name', read from /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def run(shapes, Ms, group: int, seed: int = 0, repeats: int = 5) -> dict:
     """Times the reference CPU path for every (K, N) shape at every M (one call = act round trip +
-    dequant + matmul, as each reference CPU call dequantizes); returns bytes, seconds, cores."""
+    dequant + matmul, as each reference CPU call dequantizes), `repeats` times over the whole set;
+    returns bytes per pass, the median pass time (seconds, dequant_s, matmul_s taken from that
+    pass), every pass's total, cores and the CPU model."""
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     g = torch.Generator().manual_seed(seed)
-    t_deq = t_mm = 0.0
-    nbytes = 0
+    weights = []
     for K, N in shapes:
         codes = torch.randint(0, 16, (N, K), generator=g, dtype=torch.int32)
         w = ((codes.reshape(N, K // 8, 8) << torch.arange(0, 32, 4, dtype=torch.int32)).sum(-1)).to(torch.int32)
         s = (torch.randn(K // group, N, generator=g).abs() * 0.02).to(torch.float16)
+        xs = [torch.randn(M, K, generator=g).to(torch.bfloat16) for M in Ms]
+        weights.append((K, N, w, s, xs))
         del codes
-        for M in Ms:
-            x = torch.randn(M, K, generator=g).to(torch.bfloat16)
-            t0 = time.perf_counter()
-            xd = _e4m3_roundtrip(x)
-            wd = _dequant_int4(w, s, group)
-            t1 = time.perf_counter()
-            y = (xd @ wd.t()).to(torch.bfloat16)
-            t2 = time.perf_counter()
-            t_deq += t1 - t0
-            t_mm += t2 - t1
-            nbytes += N * K // 2 + (K // group) * N * 2 + M * K * 2 + M * N * 2
-            del y, wd
-    return {"bytes": nbytes, "seconds": t_deq + t_mm, "dequant_s": t_deq, "matmul_s": t_mm, "cores": cores}
+    passes = []
+    for _ in range(repeats):
+        t_deq = t_mm = 0.0
+        nbytes = 0
+        for K, N, w, s, xs in weights:
+            for M, x in zip(Ms, xs):
+                t0 = time.perf_counter()
+                xd = _e4m3_roundtrip(x)
+                wd = _dequant_int4(w, s, group)
+                t1 = time.perf_counter()
+                y = (xd @ wd.t()).to(torch.bfloat16)
+                t2 = time.perf_counter()
+                t_deq += t1 - t0
+                t_mm += t2 - t1
+                nbytes += N * K // 2 + (K // group) * N * 2 + M * K * 2 + M * N * 2
+                del y, wd
+        passes.append((t_deq + t_mm, t_deq, t_mm, nbytes))
+    passes.sort()
+    tot, deq, mm, nbytes = passes[len(passes) // 2]
+    return {"bytes": nbytes, "seconds": tot, "dequant_s": deq, "matmul_s": mm, "cores": cores,
+            "repeats": repeats, "all_seconds": [round(p[0], 4) for p in passes], "cpu_model": cpu_model()}
