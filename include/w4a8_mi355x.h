@@ -209,6 +209,22 @@ int w4a16_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, 
                  const void* scales, int scale_fmt, const int32_t* zeros, int wfmt, int64_t group_size, void* out,
                  int64_t ldo, int silu, void* workspace, int64_t workspace_bytes, int kernel, void* stream);
 
+/* Middle step of the grouped W4A16 MoE: replaces the silu_and_mul tail between
+ * fp8_wmma.mmq_regdirect_w4a16_moe's two GEMMs (python/minisgl/quant/kernels.py:957-975) and feeds
+ * gemm2 unquantized activations. The caller runs gemm1 (w4a8_moe_gemm, f32 out, no silu) over the
+ * w4a16_act_split rows of x under a virtual route of Tt = 2 (bf16) or 3 (fp16) tokens per token:
+ * virtual token Tt*m + t has token m's expert ids and reads split row Tt*m + t. y: that gemm1's
+ * (P, 2*inter) f32 output (row stride ldy); inv_pos: its align's (T*Tt*top_k,) inverse positions.
+ * For slot (m, j): gate|up = sum over t in order of y[inv_pos[(Tt*m + t)*top_k + j]], h =
+ * silu(gate) * up rounded as the fused silu arms round (gate and up to the dtype, silu in f32,
+ * rounded, times up, rounded), then h is split as w4a16_act_split splits a row, term t written to
+ * row inv_pos[(Tt*m + t)*top_k + j] of a_fp8 with its scale in a_scales at that index, so gemm2
+ * (w4a8_moe_gemm, a_by_token 0) over the same route reads the slot's terms by padded position.
+ * h (optional, may be NULL): h at row m*top_k + j. Dropped slots (inv_pos < 0) are skipped.
+ * inter % 8 == 0 and inter <= 32768; y 16-byte, a_fp8 8-byte, h 16-byte aligned rows. */
+int w4a16_moe_silu_split(const float* y, int64_t ldy, const int32_t* inv_pos, int64_t T, int top_k, int64_t inter,
+                         int dtype, uint8_t* a_fp8, int64_t lda, float* a_scales, void* h, int64_t ldh, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

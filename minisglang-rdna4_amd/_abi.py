@@ -58,6 +58,8 @@ SIGNATURES = {
     "w4a16_linear_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_int]),
     "w4a16_linear": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _c_i64, _vp, _c_i64, _vp, _c_int, _vp, _c_int, _c_i64,
                               _vp, _c_i64, _c_int, _vp, _c_i64, _c_int, _vp]),
+    "w4a16_moe_silu_split": (_c_int, [_vp, _c_i64, _vp, _c_i64, _c_int, _c_i64, _c_int, _vp, _c_i64, _vp, _vp,
+                                      _c_i64, _vp]),
 }
 
 _lock = threading.Lock()

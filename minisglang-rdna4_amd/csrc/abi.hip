@@ -35,6 +35,9 @@ int w4a16_terms(int dtype);
 int launch_act_split(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx, uint8_t* q, int64_t ldq,
                      float* scales, hipStream_t stream);
 int launch_tsum(const float* y, int64_t N, int64_t M, int dtype, void* out, int64_t ldo, int silu, hipStream_t st);
+int64_t w4a16_moe_max_inter();
+int launch_moe_silu_split(const float* y, int64_t ldy, const int32_t* inv_pos, int64_t T, int top_k, int64_t I,
+                          int dtype, uint8_t* q, int64_t ldq, float* scales, void* h, int64_t ldh, hipStream_t st);
 int launch_moe_prep(const void* logits, int ldtype, int64_t T, int E, int top_k, int renorm, float* tw,
                     int32_t* ids, int bm, int64_t P, int32_t* sorted_ids, int32_t* expert_ids, int32_t* ntp,
                     int32_t* inv_pos, const void* x, int xdtype, int64_t K, int64_t ldx, uint8_t* xq, int64_t ldq,
@@ -272,6 +275,26 @@ int w4a16_act_split(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ld
     return fail(kErrInvalid, "w4a16_act_split: x_fp8 rows must be 8-byte aligned with stride >= K (ldq=%lld), scales non-null",
                 (long long)ldq);
   return hip_status(launch_act_split(x, x_dtype, M, K, ldx, x_fp8, ldq, scales, (hipStream_t)stream), "w4a16_act_split");
+}
+
+int w4a16_moe_silu_split(const float* y, int64_t ldy, const int32_t* inv_pos, int64_t T, int top_k, int64_t inter,
+                         int dtype, uint8_t* a_fp8, int64_t lda, float* a_scales, void* h, int64_t ldh, void* stream) {
+  if (dtype != kBF16 && dtype != kF16) return fail(kErrInvalid, "w4a16_moe_silu_split: dtype must be bf16 or fp16");
+  if (T < 0 || top_k <= 0) return fail(kErrInvalid, "w4a16_moe_silu_split: T=%lld top_k=%d", (long long)T, top_k);
+  if (inter <= 0 || inter % 8 || inter > w4a16_moe_max_inter())
+    return fail(kErrInvalid, "w4a16_moe_silu_split: inter=%lld must be a positive multiple of 8 up to %lld",
+                (long long)inter, (long long)w4a16_moe_max_inter());
+  if (ldy < 2 * inter || ldy % 4 || !aligned16(y) || !inv_pos)
+    return fail(kErrInvalid, "w4a16_moe_silu_split: y rows must be 16-byte aligned with stride >= 2*inter (ldy=%lld)",
+                (long long)ldy);
+  if (lda < inter || lda % 8 || (reinterpret_cast<uintptr_t>(a_fp8) & 7u) || !a_scales)
+    return fail(kErrInvalid, "w4a16_moe_silu_split: a_fp8 rows must be 8-byte aligned with stride >= inter (lda=%lld)",
+                (long long)lda);
+  if (h && (ldh < inter || ldh % 8 || !aligned16(h)))
+    return fail(kErrInvalid, "w4a16_moe_silu_split: h rows must be 16-byte aligned with stride >= inter (ldh=%lld)",
+                (long long)ldh);
+  return hip_status(launch_moe_silu_split(y, ldy, inv_pos, T, top_k, inter, dtype, a_fp8, lda, a_scales, h, ldh,
+                                          (hipStream_t)stream), "w4a16_moe_silu_split");
 }
 
 int w4a16_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const void* w_tile, int64_t N,

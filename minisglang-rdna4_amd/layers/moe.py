@@ -15,6 +15,7 @@ call). Zero points that are all 8 collapse to None (the kernels' symmetric path 
 from __future__ import annotations
 
 import importlib
+import logging
 
 import torch
 
@@ -175,10 +176,26 @@ class _GroupedNvFp4Experts:
         del self.weight_packed, self.weight_scale, self.weight_global
 
 
-def _no_moe_w4a16(scheme: str) -> None:
-    if kernels.MOE_W4A16 != "0":
-        raise NotImplementedError(f"MoE {scheme}: the W4A16 expert arm (MINISGL_MOE_W4A16) is not built for MI355X; "
-                                  f"unset MINISGL_MOE_W4A16 to serve the experts through the W4A8 path")
+def _moe_w4a16() -> bool:
+    """The W4A16 expert arm (unquantized activations), opt-in through MINISGL_MOE_W4A16 as in the
+    reference (python/minisgl/layers/moe.py:649-670, 745-760, 816-873)."""
+    return kernels.MOE_W4A16 != "0"
+
+
+# Widest forward the NVFP4 experts serve through the W4A16 arm (python/minisgl/layers/moe.py:809-813);
+# above it they stay W4A8 and the split is logged once.
+_NVFP4_A16_DECODE_MAX = 2
+_log = logging.getLogger("w4a8.nvfp4-moe")
+
+
+def _w4a16_experts(quant, w13, w2, x, topk_weights, topk_ids, router_logits, top_k, renormalize, e2m1):
+    """kernels.w4a16_moe over an int4 or MXFP4 expert pair (python/minisgl/layers/moe.py:663-670,
+    752-760)."""
+    inter = w13._scales_op.shape[2] // 2  # (E, G, 2*inter) group-major
+    return kernels.w4a16_moe(x, w13._w_op, w13._scales_op, getattr(w13, "_zeros_op", None), w2._w_op, w2._scales_op,
+                             getattr(w2, "_zeros_op", None), x.shape[1], inter, quant.group_size,
+                             topk_weights=topk_weights, topk_ids=topk_ids, router_logits=router_logits, top_k=top_k,
+                             renormalize=renormalize, weight_is_e2m1=e2m1)
 
 
 class MoEQuantMethod:
@@ -239,8 +256,11 @@ class _W4A8MoEMethod(MoEQuantMethod):
     def apply(self, w13, w2, hidden_states, *, router_logits, topk_weights, topk_ids, top_k, renormalize,
               activation, apply_router_weight_on_input, x_fp8=None, act_scales=None):
         _check_activation("W4A8", activation)
-        _no_moe_w4a16("W4A8")
         assert not apply_router_weight_on_input, "MoE W4A8 path has no router-weight-on-input"
+        if _moe_w4a16():
+            # fp16 activations, never quantized: a producer's fp8 pair has nothing to feed and is dropped
+            return _w4a16_experts(self._quant, w13, w2, hidden_states, topk_weights, topk_ids, router_logits, top_k,
+                                  renormalize, False)
         return kernels.w4a8_moe(hidden_states, w13._w_op, w13._scales_op, w13._zeros_op,
                                 w2._w_op, w2._scales_op, w2._zeros_op, router_logits, top_k, renormalize,
                                 topk_weights=topk_weights, topk_ids=topk_ids, activation=activation,
@@ -248,6 +268,9 @@ class _W4A8MoEMethod(MoEQuantMethod):
 
     def ep_local(self, w13, w2, g_hidden, local_weights, local_ids, *, top_k, renormalize, activation="silu"):
         _check_activation("W4A8", activation)
+        if _moe_w4a16():
+            return _w4a16_experts(self._quant, w13, w2, g_hidden, local_weights, local_ids, None, top_k, renormalize,
+                                  False)
         return kernels.w4a8_moe(g_hidden, w13._w_op, w13._scales_op, w13._zeros_op,
                                 w2._w_op, w2._scales_op, w2._zeros_op, None, top_k, renormalize,
                                 topk_weights=local_weights, topk_ids=local_ids, activation=activation)
@@ -269,14 +292,19 @@ class _MxFp4MoEMethod(MoEQuantMethod):
     def apply(self, w13, w2, hidden_states, *, router_logits, topk_weights, topk_ids, top_k, renormalize,
               activation, apply_router_weight_on_input, x_fp8=None, act_scales=None):
         _check_activation("MXFP4", activation)
-        _no_moe_w4a16("MXFP4")
         assert not apply_router_weight_on_input, "MoE MXFP4 path has no router-weight-on-input"
+        if _moe_w4a16():
+            return _w4a16_experts(self._quant, w13, w2, hidden_states, topk_weights, topk_ids, router_logits, top_k,
+                                  renormalize, True)
         return kernels.w4a8_moe(hidden_states, w13._w_op, w13._scales_op, None, w2._w_op, w2._scales_op, None,
                                 router_logits, top_k, renormalize, topk_weights=topk_weights, topk_ids=topk_ids,
                                 weight_is_e2m1=True, activation=activation, x_fp8=x_fp8, act_scales=act_scales)
 
     def ep_local(self, w13, w2, g_hidden, local_weights, local_ids, *, top_k, renormalize, activation="silu"):
         _check_activation("MXFP4", activation)
+        if _moe_w4a16():
+            return _w4a16_experts(self._quant, w13, w2, g_hidden, local_weights, local_ids, None, top_k, renormalize,
+                                  True)
         return kernels.w4a8_moe(g_hidden, w13._w_op, w13._scales_op, None, w2._w_op, w2._scales_op, None,
                                 None, top_k, renormalize, topk_weights=local_weights, topk_ids=local_ids,
                                 weight_is_e2m1=True, activation=activation)
@@ -292,6 +320,7 @@ class _NvFp4MoEMethod(MoEQuantMethod):
 
     def __init__(self, quant):
         self._quant = quant
+        self._w4a16_split_logged = False
 
     def create_experts(self, num_experts, out_features, in_features):
         return _GroupedNvFp4Experts(num_experts, out_features, in_features, self._quant)
@@ -299,8 +328,15 @@ class _NvFp4MoEMethod(MoEQuantMethod):
     def apply(self, w13, w2, hidden_states, *, router_logits, topk_weights, topk_ids, top_k, renormalize,
               activation, apply_router_weight_on_input, x_fp8=None, act_scales=None):
         _check_activation("NVFP4", activation)
-        _no_moe_w4a16("NVFP4")
         assert not apply_router_weight_on_input, "MoE NVFP4 path has no router-weight-on-input"
+        if _moe_w4a16() and hidden_states.shape[0] <= _NVFP4_A16_DECODE_MAX:
+            return kernels.w4a16_moe_decode(hidden_states, *self.plane(w13), *self.plane(w2), hidden_states.shape[1],
+                                            topk_weights=topk_weights, topk_ids=topk_ids, router_logits=router_logits,
+                                            top_k=top_k, renormalize=renormalize)
+        if _moe_w4a16() and not self._w4a16_split_logged:
+            self._w4a16_split_logged = True
+            _log.warning("MoE W4A16 on NVFP4 serves forwards of up to %d tokens; this one has %d and runs W4A8, so "
+                         "activation precision splits by batch size", _NVFP4_A16_DECODE_MAX, hidden_states.shape[0])
         return kernels.w4a8_moe(hidden_states, w13._w_op, w13._scales_op, w13._zeros_op, w2._w_op, w2._scales_op,
                                 w2._zeros_op, router_logits, top_k, renormalize, topk_weights=topk_weights,
                                 topk_ids=topk_ids, weight_is_e2m1=True, activation=activation, x_fp8=x_fp8,
@@ -308,7 +344,6 @@ class _NvFp4MoEMethod(MoEQuantMethod):
 
     def ep_local(self, w13, w2, g_hidden, local_weights, local_ids, *, top_k, renormalize, activation="silu"):
         _check_activation("NVFP4", activation)
-        _no_moe_w4a16("NVFP4")
         return kernels.w4a8_moe(g_hidden, w13._w_op, w13._scales_op, w13._zeros_op, w2._w_op, w2._scales_op,
                                 w2._zeros_op, None, top_k, renormalize, topk_weights=local_weights,
                                 topk_ids=local_ids, weight_is_e2m1=True, activation=activation)

@@ -782,3 +782,160 @@ def _moe_forward(x, w13, w13_scales, w13_zeros, w2, w2_scales, w2_zeros, gating_
     return {"out": out, "buf2": buf2, "y2": y2, "topk_weights": topk_weights, "topk_ids": topk_ids,
             "sorted_ids": sorted_ids, "expert_ids": expert_ids, "ntp": ntp, "inv_pos": inv, "block_m": block_m,
             "fused_gemm2": False}
+
+
+def _w4a16_moe_forward(x, w13, w13_scales, w13_zeros, w2, w2_scales, w2_zeros, *, dt, topk_weights=None,
+                       topk_ids=None, router_logits=None, top_k=0, renormalize=False, weight_is_e2m1=False,
+                       block_m=None, keep_h=False, what="w4a16_moe") -> dict:
+    """The grouped W4A16 MoE on the W4A8 kernels; returns the output and the intermediates.
+
+    The activations (x in `dt`) are never rounded to fp8: each token row is split exactly into
+    T = 2 (bf16) or 3 (fp16) fp8 rows (w4a16_act_split) and the route is widened to T virtual
+    tokens per token (virtual token T*m + t: token m's experts, split row T*m + t), so gemm1 is the
+    ordinary grouped GEMM with f32 output. w4a16_moe_silu_split sums each slot's T gate|up rows,
+    applies silu * up in `dt` and splits the result back into T fp8 rows at the same padded
+    positions; gemm2 runs over the same route (f32 out), and the combine weighs the T*top_k rows of
+    a token with its top-k weights repeated per term."""
+    M, K = x.shape
+    E = w13.shape[0]
+    _grp = (K // w13_scales.shape[1]) if w13_scales.dim() == 3 else -1
+    assert _grp in (16, 32, 64, 128), (
+        f"{what}: derived group_size={_grp} from K={K} and G={w13_scales.shape[1]}; scales must be GROUP-major "
+        f"(E, K//group, N), got {tuple(w13_scales.shape)}")
+    _check_moe_scale_pair(w13, w13_scales, w13_zeros, "w13")
+    _check_moe_scale_pair(w2, w2_scales, w2_zeros, "w2")
+    if x.dtype not in (torch.bfloat16, torch.float16):
+        raise TypeError(f"{what}: x must be bf16/fp16, got {x.dtype}")
+    N1 = _n_of(w13)
+    inter = N1 // 2
+    if _n_of(w2) != K:
+        raise AssertionError(f"{what}: w2 has {_n_of(w2)} output channels, expected hidden size {K}")
+    _grp2 = inter // w2_scales.shape[1]
+    if topk_ids is None:
+        assert router_logits is not None and top_k > 0, (
+            f"{what} needs a precomputed route (topk_ids/topk_weights) or router_logits + top_k")
+        topk_weights, topk_ids = _moe_route(router_logits, top_k, renormalize, E)
+    else:
+        assert topk_weights is not None, "topk_weights required when topk_ids is given"
+        topk_weights = topk_weights.to(torch.float32).contiguous()
+        topk_ids = topk_ids.to(torch.int32).contiguous()
+    top_k = topk_ids.shape[1]
+    nt = 2 if dt == torch.bfloat16 else 3
+    xa, xsc = w4a16_act_split(x.to(dt))
+    ids_v = topk_ids.repeat_interleave(nt, dim=0).contiguous()  # (nt*M, top_k)
+    numel = ids_v.numel()
+    if block_m is None:
+        block_m = _moe_block_m_auto(nt * M, E, top_k)
+    engaged("w4a8_mi355x.moe_align")
+    sorted_ids, expert_ids, ntp, inv = _moe_align(ids_v, E, block_m)
+    P = sorted_ids.shape[0]
+
+    wfmt = _abi.W_E2M1 if weight_is_e2m1 else _abi.W_INT4
+    t13 = _as_tiles(w13, K, weight_is_e2m1, 3, f"{what} w13")
+    t2 = _as_tiles(w2, inter, weight_is_e2m1, 3, f"{what} w2")
+    s13f = _scale_fmt(w13_scales, weight_is_e2m1, f"{what} w13", w13_zeros is not None)
+    s2f = _scale_fmt(w2_scales, weight_is_e2m1, f"{what} w2", w2_zeros is not None)
+    if s13f == _abi.SCALE_E4M3:
+        w13_scales = w13_scales.view(torch.uint8)
+    if s2f == _abi.SCALE_E4M3:
+        w2_scales = w2_scales.view(torch.uint8)
+    arm = _abi.KERNEL_DECODE if block_m < 64 else _abi.KERNEL_PREFILL
+    arm_name = "gemv" if arm == _abi.KERNEL_DECODE else "mfma"
+    e2 = "+e2m1" if weight_is_e2m1 else ""
+    dev = x.device
+
+    y1 = torch.empty((P, N1), dtype=torch.float32, device=dev)
+    engaged(f"w4a8_mi355x.w4a16_moe_gemm1({arm_name}{e2})")
+    _moe_gemm(xa, K, xsc, 1, sorted_ids, expert_ids, ntp, numel, top_k, block_m, P, t13, E, N1, K,
+              w13_scales.contiguous(), s13f, w13_zeros.contiguous() if w13_zeros is not None else None, wfmt, _grp,
+              y1, _abi.F32, N1, False, arm, f"{what} gemm1")
+    q2 = torch.empty((P, inter), dtype=torch.uint8, device=dev)
+    s2 = torch.empty((P,), dtype=torch.float32, device=dev)
+    h = torch.empty((M * top_k, inter), dtype=dt, device=dev) if keep_h else None
+    lib = _abi.load()
+    engaged("w4a8_mi355x.w4a16_moe_silu_split")
+    _abi.check(lib.w4a16_moe_silu_split(_abi.ptr(y1), N1, _abi.ptr(inv), M, top_k, inter, _abi.dtype_code(dt),
+                                        _abi.ptr(q2), inter, _abi.ptr(s2), _abi.ptr(h), inter, _abi.stream_of(x)),
+               f"{what} silu_split")
+    y2 = torch.empty((P, K), dtype=torch.float32, device=dev)
+    engaged(f"w4a8_mi355x.w4a16_moe_gemm2({arm_name}{e2})")
+    _moe_gemm(q2, inter, s2, 0, sorted_ids, expert_ids, ntp, numel, top_k, block_m, P, t2, E, K, inter,
+              w2_scales.contiguous(), s2f, w2_zeros.contiguous() if w2_zeros is not None else None, wfmt, _grp2,
+              y2, _abi.F32, K, False, arm, f"{what} gemm2")
+    # combine over the T*top_k virtual slots of each token: slot (T*m + t, j) sits at
+    # inv[m*(T*top_k) + t*top_k + j] and carries weight topk_weights[m, j]
+    tw_v = topk_weights.repeat(1, nt).contiguous()
+    out = torch.empty((M, K), dtype=x.dtype, device=dev)
+    engaged("w4a8_mi355x.moe_combine")
+    _abi.check(lib.w4a8_moe_combine(_abi.ptr(y2), K, _abi.ptr(inv), _abi.ptr(tw_v), M, nt * top_k, K, _abi.ptr(out),
+                                    _abi.dtype_code(x.dtype), _abi.stream_of(x)), f"{what} combine")
+    return {"out": out, "h": h, "topk_weights": topk_weights, "topk_ids": topk_ids, "sorted_ids": sorted_ids,
+            "expert_ids": expert_ids, "ntp": ntp, "inv_pos": inv, "block_m": block_m, "terms": nt}
+
+
+def w4a16_moe(
+    x: torch.Tensor,  # (M, K) activations, never quantized (cast to fp16 as the reference does)
+    w13: torch.Tensor,  # (E, 2*inter, K//8) i32 op layout (gate | up), or W4 tiles
+    w13_scales: torch.Tensor,  # (E, K//g, 2*inter) group-major fp16, or uint8 E8M0 (e2m1)
+    w13_zeros: torch.Tensor | None,  # (E, K//g, 2*inter/8) i32 AWQ zeros | None (symmetric)
+    w2: torch.Tensor,  # (E, K, inter//8) i32 op layout, or W4 tiles
+    w2_scales: torch.Tensor,  # (E, inter//g, K)
+    w2_zeros: torch.Tensor | None,
+    hidden: int,
+    inter: int,
+    group_size: int,
+    *,
+    topk_weights: torch.Tensor | None = None,
+    topk_ids: torch.Tensor | None = None,
+    router_logits: torch.Tensor | None = None,
+    top_k: int = 0,
+    renormalize: bool = False,
+    weight_is_e2m1: bool = False,
+) -> torch.Tensor:
+    """Grouped W4A16 MoE (python/minisgl/quant/kernels.py:899-1012): x cast to fp16 and never
+    quantized, route (precomputed, or softmax + top-k from router_logits), gemm1 with silu(gate) *
+    up rounded to fp16, gemm2 on those fp16 activations, top-k weighted combine in f32, cast to x's
+    dtype. int4 (symmetric or with AWQ zeros) or MXFP4 (weight_is_e2m1) weights, the same tiles and
+    scales as w4a8_moe. Returns (M, hidden)."""
+    if x.shape[1] != hidden:
+        raise AssertionError(f"w4a16_moe: hidden={hidden} does not match x's {x.shape[1]} columns")
+    if _n_of(w13) != 2 * inter:
+        raise AssertionError(f"w4a16_moe: inter={inter} does not match w13's {_n_of(w13)} rows (2*inter)")
+    derived = hidden // w13_scales.shape[1] if w13_scales.dim() == 3 else -1
+    if derived != group_size:
+        raise AssertionError(f"w4a16_moe: group_size={group_size} does not match the scales' {derived}")
+    return _w4a16_moe_forward(x, w13, w13_scales, w13_zeros, w2, w2_scales, w2_zeros, dt=torch.float16,
+                              topk_weights=topk_weights, topk_ids=topk_ids, router_logits=router_logits, top_k=top_k,
+                              renormalize=renormalize, weight_is_e2m1=weight_is_e2m1)["out"]
+
+
+def w4a16_moe_decode(
+    x: torch.Tensor,  # (M, K) bf16/fp16 activations, never quantized, kept in their dtype
+    w13_op: torch.Tensor,  # (E, 2*inter, K//8) i32 e2m1 codes, or W4 tiles
+    w13_scales: torch.Tensor,  # (E, K//16, 2*inter) e4m3 block scales, group-major
+    w13_global: torch.Tensor,  # (E, 2*inter) f32 global bitcast to int32
+    w2_op: torch.Tensor,  # (E, K, inter//8)
+    w2_scales: torch.Tensor,  # (E, inter//16, K)
+    w2_global: torch.Tensor,  # (E, K)
+    hidden: int,
+    *,
+    topk_weights: torch.Tensor | None = None,
+    topk_ids: torch.Tensor | None = None,
+    router_logits: torch.Tensor | None = None,
+    top_k: int = 0,
+    renormalize: bool = False,
+) -> torch.Tensor:
+    """Grouped W4A16 MoE for NVFP4 experts (python/minisgl/quant/kernels.py:1015-1122): x in its own
+    dtype and never quantized, silu(gate) * up rounded to that dtype, gemm2 on it, top-k weighted
+    combine in f32, cast to x's dtype. The (E, N) globals ride the zeros slot as in w4a8_moe.
+    Returns (M, hidden)."""
+    for nm, t in (("w13_op", w13_op), ("w13_scales", w13_scales), ("w13_global", w13_global), ("w2_op", w2_op),
+                  ("w2_scales", w2_scales), ("w2_global", w2_global)):
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"w4a16_moe_decode: {nm} must be a Tensor, got {type(t).__name__} ({t!r})")
+    assert isinstance(hidden, int), f"hidden must be int, got {type(hidden).__name__} ({hidden!r})"
+    if x.shape[1] != hidden:
+        raise AssertionError(f"w4a16_moe_decode: hidden={hidden} does not match x's {x.shape[1]} columns")
+    return _w4a16_moe_forward(x, w13_op, w13_scales, w13_global, w2_op, w2_scales, w2_global, dt=x.dtype,
+                              topk_weights=topk_weights, topk_ids=topk_ids, router_logits=router_logits, top_k=top_k,
+                              renormalize=renormalize, weight_is_e2m1=True, what="w4a16_moe_decode")["out"]

@@ -56,6 +56,9 @@ def lib() -> ctypes.CDLL:
         L.w4o_moe_forward.restype = None
         L.w4o_moe_forward.argtypes = [vp, ci, i64, i64, i64, i64, i64, vp, vp, vp, ctypes.c_int32, i64,
                                       vp, vp, vp, vp, vp, vp, ci, ci, i64, i64, vp, vp]
+        L.w4o_w4a16_moe_forward.restype = None
+        L.w4o_w4a16_moe_forward.argtypes = [vp, ci, i64, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, ci, ci,
+                                            i64, i64, vp, vp]
         L.w4o_rms_norm.restype = None
         L.w4o_rms_norm.argtypes = [vp, vp, vp, ci, f, ci, i64, i64, vp]
         L.w4o_act_split.restype = None
@@ -205,6 +208,31 @@ def moe_forward(x_bits, dtype, tw, sorted_ids, expert_ids, ntp, bm, top_k, w13, 
                           _p(np.ascontiguousarray(expert_ids, dtype=np.int32)), ntp, bm, _p(w13c), _p(a13), _p(z13c),
                           _p(w2c), _p(a2), _p(z2c), fmt, int(e2m1), g1, g2, _p(out), _p(buf2))
     return (out, buf2) if with_buf2 else out
+
+
+def w4a16_moe_forward(x_bits, dtype, tw, ids, w13, s13, z13, w2, s2, z2, e2m1=False, nvfp4=False):
+    """Grouped W4A16 MoE forward in f64 -> ((T, H) f64 before the dtype cast, (T*top_k, I) h bits):
+    x decoded exactly from its bf16 (dtype 0) / fp16 (dtype 1) bits, slots straight from the route
+    ids (T, top_k). Weights and scales as in moe_forward."""
+    x = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    T, H = x.shape
+    E, N1 = w13.shape[0], w13.shape[1]
+    I = N1 // 2
+    g1 = H // s13.shape[1]
+    g2 = I // s2.shape[1]
+    fmt = 2 if nvfp4 else 0 if s13.dtype == np.float16 else 1
+    conv = (lambda a: np.ascontiguousarray(a).view(np.uint16)) if fmt == 0 else (lambda a: np.ascontiguousarray(a, dtype=np.uint8))
+    zc = (lambda z: np.ascontiguousarray(np.asarray(z, dtype=np.float32)).view(np.int32)) if nvfp4 else \
+        (lambda z: np.ascontiguousarray(z, dtype=np.int32))
+    idc = np.ascontiguousarray(ids, dtype=np.int32)
+    top_k = idc.shape[1]
+    out = np.empty((T, H), dtype=np.float64)
+    h = np.zeros((T * top_k, I), dtype=np.uint16)
+    lib().w4o_w4a16_moe_forward(_p(x), dtype, T, H, I, E, top_k, _p(np.ascontiguousarray(tw, dtype=np.float32)),
+                                _p(idc), _p(np.ascontiguousarray(w13, dtype=np.int32)), _p(conv(s13)),
+                                _p(None if z13 is None else zc(z13)), _p(np.ascontiguousarray(w2, dtype=np.int32)),
+                                _p(conv(s2)), _p(None if z2 is None else zc(z2)), fmt, int(e2m1), g1, g2, _p(out), _p(h))
+    return out, h
 
 
 def silu_mul(gate: float, up: float, dtype: int = 0) -> int:

@@ -21,6 +21,9 @@
  *   gemm            -- brute force on tiny inputs against a dequantize-then-matmul numpy path,
  *                      and the invariants M-invariance / row-split / linearity in the weights.
  *   moe align       -- the worked example in python/minisgl/moe/fused.py:80-97.
+ *   w4a16 moe       -- composition of pinned pieces: a single routed expert with weight 1 equals the
+ *                      dense chain w4a16_gemm -> silu_mul -> w4a16_gemm (numpy f64 matmuls over
+ *                      w4o_dequant); linearity in the top-k weights; dropped slots contribute 0.
  *   w4a16 split     -- the identity x == sum_t scale_t * e4m3(code_t) (exact for every bf16 value
  *                      and every fp16 value whose scaled magnitude is >= 2^-6), the scale being the
  *                      smallest power of two with amax/scale <= 448 (checked against frexp), and
@@ -387,6 +390,65 @@ void w4o_moe_forward(const uint16_t* x, int dtype, int64_t T, int64_t H, int64_t
     for (int64_t j = 0; j < H; ++j) out[t * H + j] += wgt * y2[j];
   }
   free(y2); free(b2q); free(b2); free(h); free(xs); free(xq);
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* Grouped W4A16 MoE forward: restates python/minisgl/quant/kernels.py:899-1012 (w4a16_moe: x in */
+/* the activation dtype, never quantized -> gemm1 -> silu(gate) * up rounded to the dtype as the  */
+/* fused silu arms round (w4o_silu_mul) -> gemm2 on those unquantized values -> top-k weighted     */
+/* sum) and :1015-1122 (w4a16_moe_decode, the same chain for NVFP4 weights). Both GEMMs are exact  */
+/* f64 products of the decoded activations with the dequantized weights (w4o_dequant); out is the */
+/* f64 weighted sum before the final dtype cast. Slots are taken from the route directly (the     */
+/* align only orders work). ids: (T, top_k) int32, ids outside [0, E) are dropped slots.         */
+/* Weights in op layout as in w4o_moe_forward. h_out (optional): (T*top_k, I) dtype bits.        */
+/* ------------------------------------------------------------------------------------------ */
+void w4o_w4a16_moe_forward(const uint16_t* x, int dtype, int64_t T, int64_t H, int64_t I, int64_t E,
+                           int64_t top_k, const float* tw, const int32_t* ids,
+                           const int32_t* w13, const void* s13, const int32_t* z13,
+                           const int32_t* w2, const void* s2, const int32_t* z2,
+                           int scale_fmt, int e2m1, int64_t g1, int64_t g2, double* out, uint16_t* h_out) {
+  int64_t N1 = 2 * I;
+  int64_t sz13 = N1 * (H / 8), szs13 = (H / g1) * N1, szz13 = (H / g1) * (N1 / 8);
+  int64_t sz2 = H * (I / 8), szs2 = (I / g2) * H, szz2 = (I / g2) * (H / 8);
+  if (scale_fmt == 2) { szz13 = N1; szz2 = H; }
+  int sb = scale_fmt == 0 ? 2 : 1;
+  double* d13 = (double*)malloc(sizeof(double) * (size_t)(N1 * H));
+  double* d2 = (double*)malloc(sizeof(double) * (size_t)(H * I));
+  double* xv = (double*)malloc(sizeof(double) * (size_t)H);
+  double* hv = (double*)malloc(sizeof(double) * (size_t)I);
+  double* y1 = (double*)malloc(sizeof(double) * (size_t)N1);
+  memset(out, 0, sizeof(double) * (size_t)(T * H));
+  for (int64_t e = 0; e < E; ++e) {
+    int used = 0;
+    for (int64_t s = 0; s < T * top_k && !used; ++s) used = ids[s] == e;
+    if (!used) continue;
+    w4o_dequant(w13 + e * sz13, N1, H, (const char*)s13 + e * szs13 * sb, scale_fmt,
+                z13 ? z13 + e * szz13 : NULL, e2m1, g1, d13);
+    w4o_dequant(w2 + e * sz2, H, I, (const char*)s2 + e * szs2 * sb, scale_fmt,
+                z2 ? z2 + e * szz2 : NULL, e2m1, g2, d2);
+    for (int64_t s = 0; s < T * top_k; ++s) {
+      if (ids[s] != e) continue;
+      int64_t t = s / top_k;
+      for (int64_t k = 0; k < H; ++k) xv[k] = (double)from_dt(x[t * H + k], dtype);
+      for (int64_t n = 0; n < N1; ++n) {
+        double acc = 0.0;
+        for (int64_t k = 0; k < H; ++k) acc += xv[k] * d13[n * H + k];
+        y1[n] = acc;
+      }
+      for (int64_t i = 0; i < I; ++i) {
+        uint16_t hb = w4o_silu_mul(y1[i], y1[I + i], dtype);
+        if (h_out) h_out[s * I + i] = hb;
+        hv[i] = (double)from_dt(hb, dtype);
+      }
+      double wgt = (double)tw[s];
+      for (int64_t n = 0; n < H; ++n) {
+        double acc = 0.0;
+        for (int64_t i = 0; i < I; ++i) acc += hv[i] * d2[n * I + i];
+        out[t * H + n] += wgt * acc;
+      }
+    }
+  }
+  free(y1); free(hv); free(xv); free(d2); free(d13);
 }
 
 /* ------------------------------------------------------------------------------------------ */

@@ -110,9 +110,8 @@ def test_mxfp4_linear_method(kernels, oracle, dev):
     assert_close_to_oracle(out, ref, "MXFP4 method")
 
 
-def test_moe_method_matches_operator(kernels, dev):
-    """GPTQ experts through the MoE method == w4a8_moe on the op layout (same route, same tiles)."""
-    E, H, I, T, k = 8, 256, 128, 5, 2
+def _gptq_experts(kernels, dev, E, H, I):
+    """A GPTQ MoE method and expert pair after post_load, and the op-layout (w, scales) of each."""
     g = synth.gen(71)
     m = L_.create_moe_quant_method(GPTQ)
     w13, w2 = m.create_experts(E, 2 * I, H), m.create_experts(E, H, I)
@@ -126,6 +125,13 @@ def test_moe_method_matches_operator(kernels, dev):
         ops.append((torch.stack([p[0] for p in parts]).to(dev), torch.stack([p[1] for p in parts]).to(dev)))
         c.qweight, c.scales, c.qzeros = c.qweight.to(dev), c.scales.to(dev), c.qzeros.to(dev)
         c.post_load()
+    return m, w13, w2, ops
+
+
+def test_moe_method_matches_operator(kernels, dev):
+    """GPTQ experts through the MoE method == w4a8_moe on the op layout (same route, same tiles)."""
+    E, H, I, T, k = 8, 256, 128, 5, 2
+    m, w13, w2, ops = _gptq_experts(kernels, dev, E, H, I)
     assert w13._zeros_op is None and w13._w_op.dtype == torch.uint8
     x = synth.activations(T, H, seed=8).to(dev)
     logits = synth.router_logits(T, E, seed=9).to(dev)
@@ -175,7 +181,8 @@ def test_nvfp4_linear_method(kernels, oracle, dev):
 
 def test_w4a16_opt_in_routes_methods(kernels, dev, monkeypatch):
     """MINISGL_MOE_W4A16 != "0": the dense methods run the W4A16 arm (no producer pair advertised),
-    bit-identical to w4a16_linear on the same tiles; MoE methods refuse it loudly."""
+    bit-identical to w4a16_linear on the same tiles; the int4 MoE method runs w4a16_moe (apply and
+    ep_local), bit-identical to the operator on the op layout."""
     eng = pkg("_hip_engage")
     N, K = 256, 512
     m, lay, *_ = _nv_layer(N, K, 83, dev)
@@ -188,13 +195,23 @@ def test_w4a16_opt_in_routes_methods(kernels, dev, monkeypatch):
     torch.cuda.synchronize()
     assert torch.equal(out, ref)
     assert eng.counts_delta(before).get("w4a8_mi355x.w4a16_gemv+e2m1", 0) >= 1
-    mm = L_.create_moe_quant_method(GPTQ)
-    with pytest.raises(NotImplementedError, match="W4A16"):
-        mm.apply(None, None, x, router_logits=None, topk_weights=None, topk_ids=None, top_k=2, renormalize=True,
-                 activation="silu", apply_router_weight_on_input=False)
+    E, H, I, k = 8, 256, 128, 2
+    mm, w13, w2, ops = _gptq_experts(kernels, dev, E, H, I)
+    xm = synth.activations(5, H, seed=10).to(dev)
+    logits = synth.router_logits(5, E, seed=11).to(dev)
+    before = eng.counts()
+    out = mm.apply(w13, w2, xm, router_logits=logits, topk_weights=None, topk_ids=None, top_k=k, renormalize=True,
+                   activation="silu", apply_router_weight_on_input=False)
+    ref = kernels.w4a16_moe(xm, ops[0][0], ops[0][1], None, ops[1][0], ops[1][1], None, H, I, 128,
+                            router_logits=logits, top_k=k, renormalize=True)
+    tw, ti = kernels._moe_route(logits, k, True, E)
+    out_ep = mm.ep_local(w13, w2, xm, tw, ti, top_k=k, renormalize=True)
+    torch.cuda.synchronize()
+    assert out.dtype == xm.dtype and torch.equal(out, ref) and torch.equal(out_ep, out)
+    assert eng.counts_delta(before).get("w4a8_mi355x.w4a16_moe_silu_split", 0) >= 3
 
 
-def test_nvfp4_moe_method_matches_operator(kernels, dev):
+def test_nvfp4_moe_method_matches_operator(kernels, dev, monkeypatch):
     E, H, I, T, k = 8, 256, 128, 5, 2
     g = synth.gen(91)
     m = L_.create_moe_quant_method(NV)
@@ -216,6 +233,18 @@ def test_nvfp4_moe_method_matches_operator(kernels, dev):
                            weight_is_e2m1=True)
     torch.cuda.synchronize()
     assert torch.equal(out, ref)
+    # W4A16 opt-in: forwards of up to 2 tokens run w4a16_moe_decode, wider ones stay W4A8
+    monkeypatch.setattr(kernels, "MOE_W4A16", "1")
+    for rows in (1, 2, T):
+        xs, ls = x[:rows], logits[:rows]
+        got = m.apply(w13, w2, xs, router_logits=ls, topk_weights=None, topk_ids=None, top_k=k, renormalize=True,
+                      activation="silu", apply_router_weight_on_input=False)
+        if rows <= 2:
+            want = kernels.w4a16_moe_decode(xs, *ops[0], *ops[1], H, router_logits=ls, top_k=k, renormalize=True)
+        else:
+            want = kernels.w4a8_moe(xs, *ops[0], *ops[1], ls, k, True, weight_is_e2m1=True)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"rows={rows}"
 
 
 def test_loader_builds_serving_layers(kernels, dev, tmp_path):

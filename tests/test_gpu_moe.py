@@ -313,3 +313,165 @@ def test_moe_fused_gemm2_combine_bit_exact(kernels, dev, monkeypatch, fmt, T, bm
         for f in fused:
             dmax = (f["out"].float() - plain["out"].float()).abs().max().item()
             assert torch.equal(f["out"], plain["out"]), f"{fmt} T={T} bm={bm}: fused differs, max|d| {dmax:.3e}"
+
+
+# ------------------------------------------------------------------------------- W4A16 expert arm
+def _ulps(a_bits: np.ndarray, b_bits: np.ndarray, dt) -> np.ndarray:
+    """Distance in units of the dtype's spacing at the larger operand (subnormals included)."""
+    to = lambda b: torch.from_numpy(b.astype(np.int16)).view(dt).double().numpy()
+    a, b = to(a_bits), to(b_bits)
+    mant, emin = (7, -126) if dt == torch.bfloat16 else (10, -14)
+    m = np.maximum(np.abs(a), np.abs(b))
+    e = np.maximum(np.floor(np.log2(np.maximum(m, 1e-300))), emin)
+    return np.abs(a - b) / 2.0 ** (e - mant)
+
+
+def _w4a16_stage2(oracle, h_bits, dt, tw, ids, w2, s2, z2, e2m1, nvfp4, T, H):
+    """The oracle's gemm2 + top-k combine (f64) fed with the GPU's own h rows (slot order)."""
+    code = 0 if dt == torch.bfloat16 else 1
+    hv = oracle.bf16_to_f32(h_bits) if code == 0 else h_bits.view(np.float16)
+    hv = hv.astype(np.float64)
+    k = ids.shape[1]
+    I = h_bits.shape[1]
+    out = np.zeros((T, H))
+    mag = np.zeros((T, H))  # sum of |products|: the scale of an f32 dot product's rounding error
+    for e in np.unique(ids[ids >= 0]):
+        w = oracle.dequant(w2[e], s2[e], None if z2 is None else z2[e], I // s2.shape[1], e2m1, nvfp4)
+        for sl in np.nonzero(ids.reshape(-1) == e)[0]:
+            out[sl // k] += tw.reshape(-1)[sl] * (w @ hv[sl])
+            mag[sl // k] += abs(tw.reshape(-1)[sl]) * (np.abs(w) @ np.abs(hv[sl]))
+    return out, mag
+
+
+@pytest.mark.parametrize("fmt,xdt", [("sym", None), ("asym", None), ("mxfp4", None), ("nvfp4", torch.bfloat16),
+                                     ("nvfp4", torch.float16)])
+@pytest.mark.parametrize("T", [1, 5, 64])
+def test_w4a16_moe_matches_oracle(kernels, oracle, dev, fmt, xdt, T):
+    """The W4A16 expert arm (python/minisgl/quant/kernels.py:899-1122) against the oracle's f64
+    chain, stage by stage: x in the activation dtype (fp16 for w4a16_moe; x's own dtype for the
+    NVFP4 arm), never quantized.
+
+    Stage 1, h = silu(gate) * up rounded to that dtype (the contract rounds it; gemm2 reads it):
+    gate and up are f32-accumulated fp8 MFMA sums, ~1e-5 relative from the f64 values, so a few
+    per hundred fp16 (a few per thousand bf16) land on the other neighbour, and silu's slope
+    magnifies that for negative gates. Bars: at least 90% of h equal to the oracle's, every element
+    within 8 dtype ulps of its row's largest |h|. Stage 2, gemm2 + combine from the GPU's own h:
+    every output one of the two output-dtype neighbours of the oracle's f64 value, to within 2^-15
+    of the sum of the absolute products behind it (the form of an f32 dot product's error bound;
+    the fp8 MFMA accumulates with slightly less than f32 precision), rel L2 <= 1e-3 against
+    the oracle rounded to the output dtype (the one-ulp flips of 1024-element rows). End to end:
+    rel L2 <= 2e-3 against the f64 oracle (the contract bar) and <= 1e-3 against it rounded to
+    the output dtype (the stage-1 roundings move outputs by ~1e-4 relative, which moves a few
+    percent of the bf16 output roundings). T = 64 takes the MFMA arm on fp16 (block_m 128), the
+    others the GEMV; two experts are dropped from the route (ids past E) at T = 5."""
+    e, h, i, k = 32, 1024, 768, 8
+    w13, s13, z13, w2, s2, z2, e2 = _fmt_experts(fmt, e, h, i, seed=520 + T)
+    nv = fmt == "nvfp4"
+    d = lambda t: None if t is None else t.to(dev)
+    t13 = kernels.repack_w4(w13.to(dev), weight_is_e2m1=e2)
+    t2 = kernels.repack_w4(w2.to(dev), weight_is_e2m1=e2)
+    x = synth.activations(T, h, seed=530 + T)
+    if fmt == "mxfp4":
+        x = x * 0.0625  # keeps silu(gate) * up inside fp16's range for these weights (|w| up to 6)
+    if xdt is not None:
+        x = x.to(xdt)
+    lg = synth.router_logits(T, e, seed=531 + T).to(dev)
+    tw, ids = kernels._moe_route(lg, k, True, e)
+    if T == 5:
+        ids = torch.where((ids == 3) | (ids == 11), ids + e, ids)
+    dt = x.dtype if nv else torch.float16
+    nt = 2 if dt == torch.bfloat16 else 3
+    res = kernels._w4a16_moe_forward(x.to(dev), t13, d(s13), d(z13), t2, d(s2), d(z2), dt=dt, topk_weights=tw,
+                                     topk_ids=ids, weight_is_e2m1=e2, keep_h=True)
+    if nv:
+        pub = kernels.w4a16_moe_decode(x.to(dev), t13, d(s13), d(z13), t2, d(s2), d(z2), h, topk_weights=tw,
+                                       topk_ids=ids)
+    else:
+        pub = kernels.w4a16_moe(x.to(dev), t13, d(s13), d(z13), t2, d(s2), d(z2), h, i, G if not e2 else 32,
+                                topk_weights=tw, topk_ids=ids, weight_is_e2m1=e2)
+    _sync()
+    assert res["block_m"] == kernels._moe_block_m_auto(nt * T, e, k) and res["terms"] == nt
+    assert torch.equal(pub, res["out"]) and pub.dtype == x.dtype
+    code = 0 if dt == torch.bfloat16 else 1
+    ids_np = ids.cpu().numpy()
+    ids_np = np.where(ids_np >= e, -1, ids_np)
+    tw_np = tw.cpu().numpy()
+    conv_s = (lambda t: t.view(torch.uint8).numpy()) if nv else (lambda t: t.numpy())
+    conv_z = (lambda t: None if t is None else t.view(torch.float32).numpy()) if nv else \
+        (lambda t: None if t is None else t.numpy())
+    ref, href = oracle.w4a16_moe_forward(synth.bits16(x.to(dt)), code, tw_np, ids_np, w13.numpy(), conv_s(s13),
+                                         conv_z(z13), w2.numpy(), conv_s(s2), conv_z(z2), e2m1=e2, nvfp4=nv)
+    assert np.isfinite(ref).all()
+    # stage 1
+    live = (ids_np >= 0).reshape(-1)
+    hg_all = synth.bits16(res["h"].cpu())
+    hg = hg_all[live]
+    u = _ulps(hg, href[live], dt)
+    to = lambda b: torch.from_numpy(b.astype(np.int16)).view(dt).double().numpy()
+    hv, hr = to(hg), to(href[live])
+    rowmax = np.abs(hr).max(axis=1, keepdims=True)
+    ulp_rel = 2.0 ** (-8 if dt == torch.bfloat16 else -11)
+    worst = (np.abs(hv - hr) / rowmax).max()
+    print(f"[w4a16 moe] {fmt} {dt} T={T}: h equal {np.mean(u == 0):.4f}, 1 ulp {np.mean(u == 1):.4f}, "
+          f"2 {np.mean(u == 2):.4f}, >2 {np.mean(u > 2):.5f}; max |dh| / row max {worst:.3e}", flush=True)
+    assert np.mean(u == 0) >= 0.9 and worst <= 8 * ulp_rel
+    # stage 2 from the GPU's h
+    g = res["out"].float().cpu().numpy().astype(np.float64)
+    ref2, mag = _w4a16_stage2(oracle, hg_all, dt, tw_np, ids_np, w2.numpy(), conv_s(s2), conv_z(z2), e2, nv, T, h)
+    nrm = np.linalg.norm(ref)
+    rnd = lambda a: torch.from_numpy(a).to(x.dtype).double().numpy()
+    rel2_r = np.linalg.norm(g - rnd(ref2)) / nrm
+    mant = 7 if x.dtype == torch.bfloat16 else 10
+    spacing = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(ref2), 1e-30))) - mant)
+    excess = (np.abs(g - ref2) - spacing) / mag
+    unfaithful = excess > 2.0 ** -15
+    rel = np.linalg.norm(g - ref) / nrm
+    rel_r = np.linalg.norm(g - rnd(ref)) / nrm
+    print(f"[w4a16 moe] {fmt} T={T}: stage 2 rel L2 vs rounded {rel2_r:.3e}, worst excess over a dtype "
+          f"neighbour {excess.max():.3e} of sum|products| ({int(unfaithful.sum())} over 2^-15); end to end "
+          f"{rel:.3e} (vs dtype-rounded oracle {rel_r:.3e})", flush=True)
+    assert not unfaithful.any() and rel2_r <= 1e-3
+    assert rel <= 2e-3 and rel_r <= 1e-3
+
+
+@pytest.mark.parametrize("fmt", ["sym", "mxfp4"])
+def test_w4a16_moe_closer_to_exact_than_w4a8(kernels, oracle, dev, fmt):
+    """The point of the arm (python/minisgl/quant/kernels.py:912-915): against the unquantized
+    chain of the same 4-bit experts (the oracle's f64 W4A16 forward), w4a16_moe is closer than
+    w4a8_moe, by a wide margin."""
+    e, h, i, k, T = 32, 1024, 768, 8, 16
+    w13, s13, z13, w2, s2, z2, e2 = _fmt_experts(fmt, e, h, i, seed=560)
+    d = lambda t: None if t is None else t.to(dev)
+    t13 = kernels.repack_w4(w13.to(dev), weight_is_e2m1=e2)
+    t2 = kernels.repack_w4(w2.to(dev), weight_is_e2m1=e2)
+    x = (synth.activations(T, h, seed=561) * (0.0625 if e2 else 1.0)).to(torch.float16)
+    lg = synth.router_logits(T, e, seed=562).to(dev)
+    tw, ids = kernels._moe_route(lg, k, True, e)
+    a16 = kernels.w4a16_moe(x.to(dev), t13, d(s13), d(z13), t2, d(s2), d(z2), h, i, 32 if e2 else G, topk_weights=tw,
+                            topk_ids=ids, weight_is_e2m1=e2)
+    a8 = kernels.w4a8_moe(x.to(dev), t13, d(s13), d(z13), t2, d(s2), d(z2), None, k, True, topk_weights=tw,
+                          topk_ids=ids, weight_is_e2m1=e2)
+    _sync()
+    ref, _ = oracle.w4a16_moe_forward(synth.bits16(x), 1, tw.cpu().numpy(), ids.cpu().numpy(), w13.numpy(),
+                                      s13.numpy(), None if z13 is None else z13.numpy(), w2.numpy(), s2.numpy(),
+                                      None if z2 is None else z2.numpy(), e2m1=e2)
+    assert np.isfinite(ref).all()
+    r16 = np.linalg.norm(a16.float().cpu().numpy() - ref) / np.linalg.norm(ref)
+    r8 = np.linalg.norm(a8.float().cpu().numpy() - ref) / np.linalg.norm(ref)
+    print(f"[w4a16 moe] {fmt}: |a16-exact| {r16:.3e}  |a8-exact| {r8:.3e}", flush=True)
+    assert r16 * 4 <= r8
+
+
+def test_w4a16_moe_silu_split_refusals(kernels, dev):
+    lib = pkg("_abi").load()
+    y = torch.empty((16, 64), dtype=torch.float32, device=dev)
+    inv = torch.zeros((12,), dtype=torch.int32, device=dev)
+    q = torch.empty((16, 32), dtype=torch.uint8, device=dev)
+    s = torch.empty((16,), dtype=torch.float32, device=dev)
+    p = lambda t: t.data_ptr()
+    st = torch.cuda.current_stream().cuda_stream
+    assert lib.w4a16_moe_silu_split(p(y), 64, p(inv), 2, 2, 30, 1, p(q), 32, p(s), None, 0, st) == 1  # inter % 8
+    assert lib.w4a16_moe_silu_split(p(y), 48, p(inv), 2, 2, 32, 1, p(q), 32, p(s), None, 0, st) == 1  # ldy < 2*inter
+    assert lib.w4a16_moe_silu_split(p(y), 64, p(inv), 2, 2, 32, 5, p(q), 32, p(s), None, 0, st) == 1  # dtype
+    assert lib.w4a16_moe_silu_split(p(y), 64, p(inv), 2, 2, 32, 1, p(q), 32, None, None, 0, st) == 1  # scales
+    assert b"silu_split" in lib.w4a8_last_error()

@@ -427,3 +427,53 @@ def test_nvfp4_dequant_is_two_level(oracle):
     sc = s.to(torch.float32).numpy().astype(np.float64)  # (K/16, N)
     want = lut * sc.T.repeat(16, axis=1) * glob.numpy().astype(np.float64)[:, None]
     assert np.array_equal(got, want)
+
+
+# ------------------------------------------------------------------------------- W4A16 MoE
+def _silu_row(oracle, y1, I, dtype):
+    return np.array([oracle.silu_mul(y1[i], y1[I + i], dtype) for i in range(I)], dtype=np.uint16)
+
+
+@pytest.mark.parametrize("dtype,code", [(torch.float16, 1), (torch.bfloat16, 0)])
+def test_w4a16_moe_single_expert_is_the_dense_chain(oracle, dtype, code):
+    """One routed expert per token with weight 1: the W4A16 MoE equals the dense chain
+    w4a16_gemm -> silu_mul in the dtype -> w4a16_gemm on those values (each piece pinned above),
+    with AWQ-style zeros so a dropped zero term would show."""
+    T, H, I, E, g = 3, 256, 128, 4, 64
+    x = synth.activations(T, H, seed=41, dtype=torch.float32).to(dtype)
+    w13, s13, z13 = synth.int4_weight(2 * I, H, g, seed=42, asym=True, E=E)
+    w2, s2, z2 = synth.int4_weight(H, I, g, seed=43, asym=True, E=E)
+    w13, s13, z13, w2, s2, z2 = (t.numpy() for t in (w13, s13, z13, w2, s2, z2))
+    ids = np.array([[2], [0], [2]], dtype=np.int32)
+    xb = synth.bits16(x)
+    out, h = oracle.w4a16_moe_forward(xb, code, np.ones((T, 1), np.float32), ids, w13, s13, z13, w2, s2, z2)
+    for t in range(T):
+        e = ids[t, 0]
+        y1 = oracle.w4a16_gemm(xb[t:t + 1], code, w13[e], s13[e], z13[e], g)[0]
+        hb = _silu_row(oracle, y1, I, code)
+        assert np.array_equal(h[t], hb)
+        y2 = oracle.w4a16_gemm(hb[None, :], code, w2[e], s2[e], z2[e], g)[0]
+        np.testing.assert_allclose(out[t], y2, rtol=1e-12, atol=1e-12)
+
+
+def test_w4a16_moe_is_linear_in_the_route(oracle):
+    """top-k weights (a, b) over experts (e0, e1) give a * out(e0) + b * out(e1), and a dropped
+    slot (expert id -1) contributes nothing (MXFP4 weights, fp16 activations)."""
+    T, H, I, E = 2, 128, 64, 3
+    x = synth.activations(T, H, seed=44, dtype=torch.float32).to(torch.float16)
+    w13, s13 = synth.mxfp4_weight(2 * I, H, seed=45, E=E)
+    w2, s2 = synth.mxfp4_weight(H, I, seed=46, E=E)
+    w13, s13, w2, s2 = w13.numpy(), s13.numpy(), w2.numpy(), s2.numpy()
+    xb = synth.bits16(x)
+    tw = np.array([[0.625, 0.375], [0.25, 0.75]], dtype=np.float32)
+    ids = np.array([[1, 2], [0, 1]], dtype=np.int32)
+    both, h = oracle.w4a16_moe_forward(xb, 1, tw, ids, w13, s13, None, w2, s2, None, e2m1=True)
+    parts = [oracle.w4a16_moe_forward(xb, 1, np.ones((T, 1), np.float32), ids[:, j:j + 1], w13, s13, None, w2, s2,
+                                      None, e2m1=True) for j in range(2)]
+    want = tw[:, :1] * parts[0][0] + tw[:, 1:] * parts[1][0]
+    np.testing.assert_allclose(both, want, rtol=1e-12, atol=1e-12)
+    assert np.array_equal(h[0::2], parts[0][1]) and np.array_equal(h[1::2], parts[1][1])
+    dropped = ids.copy()
+    dropped[:, 1] = -1
+    one, _ = oracle.w4a16_moe_forward(xb, 1, tw, dropped, w13, s13, None, w2, s2, None, e2m1=True)
+    np.testing.assert_allclose(one, tw[:, :1] * parts[0][0], rtol=1e-12, atol=1e-12)
