@@ -193,16 +193,22 @@ def profile_prefill(kernels, dev, fmt: str, M: int, K: int, N: int) -> dict:
     import torch
 
     gen = torch.Generator(device=dev).manual_seed(9)
+    z = None
     if fmt == "int4":
         tiles, sc = make_weights(kernels, K, N, gen, dev)
         g, e2 = GROUP, False
+    elif fmt == "nvfp4":
+        tiles = kernels.repack_w4(_rand_words((N, K // 8), gen, dev), weight_is_e2m1=True)
+        sc = (torch.rand(K // 16, N, generator=gen, device=dev) * 6 + 0.25).to(torch.float8_e4m3fn)
+        z = torch.rand(N, generator=gen, device=dev) * 1e-3 + 1e-4
+        g, e2 = 16, True
     else:
         tiles = kernels.repack_w4(_rand_words((N, K // 8), gen, dev), weight_is_e2m1=True)
         sc = torch.randint(119, 128, (K // 32, N), generator=gen, device=dev, dtype=torch.int32).to(torch.uint8)
         g, e2 = 32, True
     x = make_x(M, K, 5, dev)
     q, s = kernels.act_quant(x)
-    us = _time_calls([lambda: kernels.w4a8_linear(x, tiles, sc, None, g, weight_is_e2m1=e2, x_fp8=q,
+    us = _time_calls([lambda: kernels.w4a8_linear(x, tiles, sc, z, g, weight_is_e2m1=e2, x_fp8=q,
                                                   act_scales=s)], 5)
     return {"profile_prefill": fmt, "M": M, "K": K, "N": N, **_tflops(2.0 * M * N * K, us)}
 
@@ -432,7 +438,7 @@ def main() -> int:
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-configs", action="store_true")
     ap.add_argument("--profile-prefill", nargs=4, metavar=("FMT", "M", "K", "N"),
-                    help="time one prefill GEMM (FMT int4 or mxfp4) and exit, for counter runs")
+                    help="time one prefill GEMM (FMT int4, mxfp4 or nvfp4) and exit, for counter runs")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:

@@ -17,22 +17,10 @@
 // step k, writes the int4 registers of step k+1, then waits for its own step-k+1 loads (a counted
 // vmcnt, the loads of step k+2 stay in flight) and meets the other waves at one s_barrier.
 #include <cstdlib>
-#include <type_traits>
 
 #include "prefill.h"
 
 namespace w4a8 {
-
-template <int N>
-using IC = std::integral_constant<int, N>;
-
-// s_waitcnt vmcnt(n) lgkmcnt(0), expcnt untouched (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] |
-// lgkmcnt[11:8] | vmcnt[5:4] << 14).
-template <int N>
-__device__ __forceinline__ void wait_vm_lgkm0() {
-  static_assert(N >= 0 && N < 64, "vmcnt");
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (0 << 8) | ((N >> 4) << 14));
-}
 
 template <int WM, int WN, int RB, int NSB, int MODE>
 __global__ void __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))

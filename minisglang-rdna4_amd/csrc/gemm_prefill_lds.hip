@@ -364,8 +364,11 @@ static int launch_lds_cfg(const GemmArgs& p, int mode, int64_t row_tiles, hipStr
 // per-wave kernel). bm_rows: rows per workgroup the caller requires (grouped: divides the align
 // block; 0 for dense).
 int launch_prefill_lds(const GemmArgs& p, int64_t rows_to_cover, int bm_rows, hipStream_t stream) {
-  // the DMA-staged pipeline first (three stages, A by LDS-DMA); this kernel covers what it leaves
-  const int rc = launch_prefill_dma(p, rows_to_cover, bm_rows, stream);
+  // NVFP4 on the fp16 MFMA, then the DMA-staged pipeline (three stages, A by LDS-DMA); this
+  // kernel covers what those leave
+  int rc = launch_prefill_nv(p, rows_to_cover, bm_rows, stream);
+  if (rc != kErrUnsupported) return rc;
+  rc = launch_prefill_dma(p, rows_to_cover, bm_rows, stream);
   if (rc != kErrUnsupported) return rc;
   int mode;
   if (p.wfmt == kInt4 && p.sfmt == kScaleF16 && p.group % kTileK == 0)

@@ -2,9 +2,22 @@
 // gemm_prefill_dma.hip): weight-format modes, grouped-row lookup, the silu epilogue, the 1 KiB
 // MFMA operand read and the per-stage LDS layout.
 #pragma once
+#include <type_traits>
+
 #include "gemm_args.h"
 
 namespace w4a8 {
+
+template <int N>
+using IC = std::integral_constant<int, N>;
+
+// s_waitcnt vmcnt(n) lgkmcnt(0), expcnt untouched (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] |
+// lgkmcnt[11:8] | vmcnt[5:4] << 14).
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (0 << 8) | ((N >> 4) << 14));
+}
 
 constexpr int kPSym = 0, kPAsym = 1, kPE8M0 = 2;
 
@@ -197,5 +210,7 @@ __device__ __forceinline__ void store_tile(const GemmArgs& p, const v4f (&acc)[R
 
 // Launch of the DMA-staged kernel (gemm_prefill_dma.hip); kErrUnsupported when it does not apply.
 int launch_prefill_dma(const GemmArgs& p, int64_t rows_to_cover, int bm_rows, hipStream_t stream);
+// NVFP4 on the fp16 MFMA (gemm_prefill_nv.hip); kErrUnsupported for other formats and shapes.
+int launch_prefill_nv(const GemmArgs& p, int64_t rows_to_cover, int bm_rows, hipStream_t stream);
 
 }  // namespace w4a8

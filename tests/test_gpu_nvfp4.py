@@ -43,6 +43,24 @@ def test_nvfp4_w4a8_matches_oracle(kernels, oracle, dev, K, N):
         assert_close_to_oracle(out, _w4a8_ref(oracle, x, w, s, glob), f"nvfp4 w4a8 K={K} N={N} M={M}")
 
 
+@pytest.mark.parametrize("K,N", [(2048, 1536), (8192, 512)])
+def test_nvfp4_prefill_fp16_mfma(kernels, oracle, dev, K, N):
+    """The prefill arm runs NVFP4 on the fp16 MFMA (e2m1 * e4m3 block scale and the e4m3
+    activation codes are exact in fp16): against the oracle at 2e-3 with the structural guard on
+    every row of M = 640 (a partial 256-row tile; 64-row tiles for the small grid of N = 512), and
+    row-split invariant bit for bit (rows 200..263 alone, a different tile shape, equal the same
+    rows of the full call)."""
+    w, s, glob = synth.nvfp4_weight(N, K, seed=K // 64 + N)
+    tiles = kernels.repack_w4(w.to(dev), weight_is_e2m1=True)
+    sd, gd = s.to(dev), glob.to(dev)
+    x = synth.activations(640, K, seed=K, outliers=True)
+    out = kernels.w4a8_linear(x.to(dev), tiles, sd, gd, 16, weight_is_e2m1=True)
+    part = kernels.w4a8_linear(x[200:264].to(dev), tiles, sd, gd, 16, weight_is_e2m1=True)
+    _sync()
+    assert torch.equal(part, out[200:264])
+    assert_close_to_oracle(out, _w4a8_ref(oracle, x, w, s, glob), f"nvfp4 prefill K={K} N={N} M=640")
+
+
 def test_nvfp4_scale_dtype_forms_agree(kernels, dev):
     """float8_e4m3fn scales, their uint8 bytes (+ populated zeros slot) and the global as f32 or as its
     int32 bit pattern are the same call (python/minisgl/quant/kernels.py:518-559)."""
