@@ -78,14 +78,22 @@ gemm_nv_kernel(const GemmArgs p) {
   constexpr int NOPS = A_PER + 3 * B_PER;
   static_assert(3 * kA + 2 * kB <= 160 * 1024, "LDS");
 
+  // every stage its own array, every stage index a compile-time constant (the K loop is unrolled
+  // by six): the compiler then tells the stages apart, so the B writes of step k+1 do not wait for
+  // the A DMAs of step k+2
   __shared__ __align__(16) unsigned char sa0[kA];
   __shared__ __align__(16) unsigned char sa1[kA];
   __shared__ __align__(16) unsigned char sa2[kA];
-  __shared__ __align__(16) unsigned char sbb[2 * kB];
+  __shared__ __align__(16) unsigned char sb0[kB];
+  __shared__ __align__(16) unsigned char sb1[kB];
   auto astage = [&](auto I) __attribute__((always_inline)) -> unsigned char* {
     if constexpr (decltype(I)::value == 0) return sa0;
     else if constexpr (decltype(I)::value == 1) return sa1;
     else return sa2;
+  };
+  auto bstage = [&](auto I) __attribute__((always_inline)) -> unsigned char* {
+    if constexpr (decltype(I)::value == 0) return sb0;
+    else return sb1;
   };
 
   const int lane = threadIdx.x & 63;
@@ -165,9 +173,10 @@ gemm_nv_kernel(const GemmArgs p) {
       rs1[R][i] = bload8(rs_s, s_voff[i] + N, so_s);
     }
   };
-  // B registers of set R -> fp16 operands in B stage `bs`
-  auto commit = [&](auto R_, unsigned char* bs) __attribute__((always_inline)) {
+  // B registers of set R -> fp16 operands in B stage BI
+  auto commit = [&](auto R_, auto BI) __attribute__((always_inline)) {
     constexpr int R = decltype(R_)::value;
+    unsigned char* bs = bstage(BI);
 #pragma unroll
     for (int i = 0; i < B_PER; ++i) {
       const int c = (int)threadIdx.x + i * T;
@@ -197,10 +206,15 @@ gemm_nv_kernel(const GemmArgs p) {
   uint32_t ob = (uint32_t)((wn * NSB * 4 * 64 + lane) * 16);
   asm volatile("" : "+v"(oa), "+v"(ob));
 
-  // the four fp16 sub-steps of K step from A stage I and B stage bs; mid() runs after the first
-  // sub-step's MFMAs are issued (the next step's B decode overlaps them)
-  auto compute = [&](auto I, const unsigned char* bs, auto mid) __attribute__((always_inline)) {
+  // the four fp16 sub-steps of a K step from A stage I and B stage BI (each sub-step's B fragments
+  // read one sub-step ahead of its MFMAs); mid() runs after the first sub-step's MFMAs are issued
+  // (the next step's B decode overlaps them)
+  auto compute = [&](auto I, auto BI, auto mid) __attribute__((always_inline)) {
     const unsigned char* sa = astage(I);
+    const unsigned char* bs = bstage(BI);
+    v8h bc[NSB], bn[NSB];
+#pragma unroll
+    for (int j = 0; j < NSB; ++j) bc[j] = *reinterpret_cast<const v8h*>(bs + ob + (j * 4) * 1024);
     uint4 alo[RB], ahi[RB];
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
@@ -209,9 +223,10 @@ gemm_nv_kernel(const GemmArgs p) {
     }
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      v8h b[NSB];
+      if (s < 3) {
 #pragma unroll
-      for (int j = 0; j < NSB; ++j) b[j] = *reinterpret_cast<const v8h*>(bs + ob + (j * 4 + s) * 1024);
+        for (int j = 0; j < NSB; ++j) bn[j] = *reinterpret_cast<const v8h*>(bs + ob + (j * 4 + s + 1) * 1024);
+      }
       v8h a[RB];
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
@@ -221,30 +236,34 @@ gemm_nv_kernel(const GemmArgs p) {
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-        for (int j = 0; j < NSB; ++j) acc[rb][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[rb], b[j], acc[rb][j], 0, 0, 0);
+        for (int j = 0; j < NSB; ++j) acc[rb][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[rb], bc[j], acc[rb][j], 0, 0, 0);
       if (s == 0) mid();
+      if (s < 3) {
+#pragma unroll
+        for (int j = 0; j < NSB; ++j) bc[j] = bn[j];
+      }
     }
   };
 
-  auto bstage = [&](int kt) __attribute__((always_inline)) { return sbb + (kt & 1) * kB; };
-  // one pipelined step kt (A stage C = kt % 3): loads of kt+2, MFMAs of kt, B registers of kt+1 to
-  // LDS, wait for kt+1's loads, barrier
-  auto step = [&](auto C, int kt) __attribute__((always_inline)) {
-    constexpr int c = decltype(C)::value, n1 = (c + 1) % 3, n2 = (c + 2) % 3;
+  // one pipelined step kt (A stage C = kt % 3, B stage D = kt % 2): loads of kt+2, MFMAs of kt,
+  // B registers of kt+1 to LDS, wait for kt+1's loads, barrier
+  auto step = [&](auto C, auto D, int kt) __attribute__((always_inline)) {
+    constexpr int c = decltype(C)::value, d = decltype(D)::value, n1 = (c + 1) % 3, n2 = (c + 2) % 3;
     issue(IC<n2>{}, kt + 2);
     __builtin_amdgcn_sched_barrier(0);
-    compute(C, bstage(kt), [&]() __attribute__((always_inline)) { commit(IC<n1>{}, bstage(kt + 1)); });
+    compute(C, D, [&]() __attribute__((always_inline)) { commit(IC<n1>{}, IC<1 - d>{}); });
     __builtin_amdgcn_sched_barrier(0);
     wait_vm_lgkm0<NOPS>();
     __builtin_amdgcn_s_barrier();
   };
-  auto step_tail = [&](auto C, int kt) __attribute__((always_inline)) {
-    constexpr int c = decltype(C)::value, n1 = (c + 1) % 3, n2 = (c + 2) % 3;
+  // the same step near the end of K: loads only while steps remain, a full wait otherwise
+  auto step_tail = [&](auto C, auto D, int kt) __attribute__((always_inline)) {
+    constexpr int c = decltype(C)::value, d = decltype(D)::value, n1 = (c + 1) % 3, n2 = (c + 2) % 3;
     if (kt >= KT) return;
     const bool more = kt + 2 < KT;
     if (more) issue(IC<n2>{}, kt + 2);
-    compute(C, bstage(kt), [&]() __attribute__((always_inline)) {
-      if (kt + 1 < KT) commit(IC<n1>{}, bstage(kt + 1));
+    compute(C, D, [&]() __attribute__((always_inline)) {
+      if (kt + 1 < KT) commit(IC<n1>{}, IC<1 - d>{});
     });
     if (more) wait_vm_lgkm0<NOPS>();
     else wait_vm_lgkm0<0>();
@@ -253,20 +272,26 @@ gemm_nv_kernel(const GemmArgs p) {
 
   issue(IC<0>{}, 0);
   issue(IC<1>{}, 1);
-  commit(IC<0>{}, bstage(0));
+  commit(IC<0>{}, IC<0>{});
   wait_vm_lgkm0<NOPS>();
   __builtin_amdgcn_s_barrier();
   int kt = 0;
-  for (; kt + 4 < KT; kt += 3) {
-    step(IC<0>{}, kt);
-    step(IC<1>{}, kt + 1);
-    step(IC<2>{}, kt + 2);
+  for (; kt + 7 < KT; kt += 6) {
+    step(IC<0>{}, IC<0>{}, kt);
+    step(IC<1>{}, IC<1>{}, kt + 1);
+    step(IC<2>{}, IC<0>{}, kt + 2);
+    step(IC<0>{}, IC<1>{}, kt + 3);
+    step(IC<1>{}, IC<0>{}, kt + 4);
+    step(IC<2>{}, IC<1>{}, kt + 5);
   }
-  step_tail(IC<0>{}, kt);
-  step_tail(IC<1>{}, kt + 1);
-  step_tail(IC<2>{}, kt + 2);
-  step_tail(IC<0>{}, kt + 3);
-  step_tail(IC<1>{}, kt + 4);
+  step_tail(IC<0>{}, IC<0>{}, kt);
+  step_tail(IC<1>{}, IC<1>{}, kt + 1);
+  step_tail(IC<2>{}, IC<0>{}, kt + 2);
+  step_tail(IC<0>{}, IC<1>{}, kt + 3);
+  step_tail(IC<1>{}, IC<0>{}, kt + 4);
+  step_tail(IC<2>{}, IC<1>{}, kt + 5);
+  step_tail(IC<0>{}, IC<0>{}, kt + 6);
+  step_tail(IC<1>{}, IC<1>{}, kt + 7);
 
   // epilogue: the per-channel global, then the row scale and the store (silu pairs strips j and
   // j + NSB/2 inside the wave)
