@@ -12,6 +12,8 @@
 //   with per-wave lane masks and per-expert prefix sums over the waves.
 // combine: out[t] = sum_j tw[t,j] * y[pos(t,j)] in f32, j in slot order, cast to the activation
 //   dtype (mmq_fp8_moe_gather_reduce, kernels.py:876-882).
+#include <cstdlib>
+
 #include "act_quant.h"
 
 namespace w4a8 {
@@ -250,6 +252,126 @@ __device__ __forceinline__ void align_block(const int32_t* ids, int64_t numel, i
 }
 
 constexpr int kAlignHeld = 32768;  // slots whose ids the histogram pass keeps in LDS (64 KiB)
+static int64_t align_multi_min() {
+  const char* e = getenv("W4A8_ALIGN_MULTI_MIN");
+  return e ? atoll(e) : 4096;
+}
+static const int64_t kAlignMultiMin = align_multi_min();  // slots above which the align spans workgroups
+
+// Align by ceil(numel / NT) workgroups, workgroup b owning slots [b*NT, b*NT + NT): every workgroup
+// reads all ids for the per-expert totals (and the counts of the slots before its own), scans the
+// padded totals exactly as align_block does, and places its own slots at expert start + slots of
+// that expert before the chunk + rank inside the chunk (the per-wave lane masks of align_block), so
+// the order is the same stable slot order and every output equals align_block's. The padding
+// sentinels, the tail, the block owners and ntp are split over the workgroups; every output element
+// is written by exactly one thread. No workgroup depends on another (no workspace, no flags).
+template <int NT, int EMAX>
+__global__ void __launch_bounds__(NT)
+moe_align_multi_kernel(const int32_t* __restrict__ ids, int64_t numel, int E, int bm, int64_t P,
+                       int32_t* __restrict__ sorted_ids, int32_t* __restrict__ expert_ids,
+                       int32_t* __restrict__ ntp_out, int32_t* __restrict__ inv_pos) {
+  constexpr int NW = NT / 64;
+  static_assert(NT >= EMAX, "one scan pass: a thread per expert");
+  __shared__ int cnt[EMAX];
+  __shared__ int before[EMAX];
+  __shared__ int base[EMAX];
+  __shared__ unsigned long long mask[NW][EMAX];
+  __shared__ int pre[NW][EMAX];
+  __shared__ int wsums[NW];
+  __shared__ int total_s;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t nb = gridDim.x, b = blockIdx.x;
+  const int64_t c0 = b * NT;
+  for (int e = tid; e < EMAX; e += NT) {
+    cnt[e] = 0;
+    before[e] = 0;
+  }
+  for (int i = tid; i < NW * EMAX; i += NT) (&mask[0][0])[i] = 0ull;
+  lds_barrier();
+  for (int64_t i0 = 0; i0 < numel; i0 += 8 * NT) {
+    int ev[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int64_t i = i0 + u * NT + tid;
+      ev[u] = i < numel ? ids[i] : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int64_t i = i0 + u * NT + tid;
+      const int e = ev[u];
+      if (e < 0 || e >= E) continue;
+      atomicAdd(&cnt[e], 1);
+      if (i < c0) atomicAdd(&before[e], 1);
+    }
+  }
+  lds_barrier();
+  // exclusive scan of padded counts over experts (one expert per thread)
+  const int padded = tid < E ? (cnt[tid] + bm - 1) / bm * bm : 0;
+  int incl = padded;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int n = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += n;
+  }
+  if (lane == 63) wsums[wave] = incl;
+  lds_barrier();
+  if (tid == 0) {
+    int run = 0;
+    for (int w = 0; w < NW; ++w) {
+      const int sw = wsums[w];
+      wsums[w] = run;
+      run += sw;
+    }
+    total_s = run;
+  }
+  lds_barrier();
+  const int start = tid < E ? incl - padded + wsums[wave] : 0;
+  const int total = total_s;
+  if (tid < E) base[tid] = start;
+  lds_barrier();
+  // this workgroup's share of the padding sentinels, the tail, the block owners and ntp
+  const int64_t stride = nb * NT;
+  for (int64_t x = b * NT + tid; x < (int64_t)E * (bm - 1); x += stride) {
+    const int e = (int)(x / (bm - 1)), j = (int)(x - (int64_t)e * (bm - 1));
+    const int c = cnt[e];
+    if (c + j < (c + bm - 1) / bm * bm) sorted_ids[base[e] + c + j] = (int32_t)numel;
+  }
+  for (int64_t i = total + b * NT + tid; i < P; i += stride) sorted_ids[i] = (int32_t)numel;
+  if (tid < E && tid % nb == b) {
+    const int b0 = start / bm, nbl = (cnt[tid] + bm - 1) / bm;
+    for (int k = 0; k < nbl; ++k) expert_ids[b0 + k] = tid;
+  }
+  const int64_t nblocks = (P + bm - 1) / bm;
+  for (int64_t k = total / bm + b * NT + tid; k < nblocks; k += stride) expert_ids[k] = E - 1;
+  if (b == 0 && tid == 0) *ntp_out = total;
+  // stable scatter of this workgroup's slots
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  const int64_t i = c0 + tid;
+  int e = -1;
+  if (i < numel) {
+    e = ids[i];
+    if (e >= E) e = -1;
+  }
+  if (e >= 0) atomicOr(&mask[wave][e], 1ull << lane);
+  lds_barrier();
+  const uint64_t m = e >= 0 ? mask[wave][e] : 0ull;
+  if (tid < E) {
+    int run = start + before[tid];
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      pre[w][tid] = run;
+      run += __popcll(mask[w][tid]);
+    }
+  }
+  lds_barrier();
+  if (e >= 0) {
+    const int off = pre[wave][e] + __popcll(m & below);
+    sorted_ids[off] = (int32_t)i;
+    if (inv_pos) inv_pos[i] = off;
+  } else if (i < numel && inv_pos) {
+    inv_pos[i] = -1;  // dropped slot: the combine skips it
+  }
+}
 
 // E <= 256: 1024 threads; E <= 512: 512 threads (the per-wave masks and offsets scale with both)
 template <int NT, int EMAX>
@@ -343,6 +465,17 @@ int launch_moe_route(const void* logits, int dtype, int64_t T, int E, int top_k,
 
 int launch_moe_align(const int32_t* ids, int64_t numel, int E, int bm, int64_t P, int32_t* sorted_ids,
                      int32_t* expert_ids, int32_t* ntp, int32_t* inv_pos, hipStream_t stream) {
+  // one workgroup per 1024 (E > 256: 512) slots above kAlignMultiMin slots; below, the one-workgroup
+  // kernel, which keeps the ids it reads in LDS
+  if (numel > kAlignMultiMin) {
+    if (E <= 256)
+      hipLaunchKernelGGL((moe_align_multi_kernel<1024, 256>), dim3((unsigned)((numel + 1023) / 1024)), dim3(1024), 0,
+                         stream, ids, numel, E, bm, P, sorted_ids, expert_ids, ntp, inv_pos);
+    else
+      hipLaunchKernelGGL((moe_align_multi_kernel<512, 512>), dim3((unsigned)((numel + 511) / 512)), dim3(512), 0,
+                         stream, ids, numel, E, bm, P, sorted_ids, expert_ids, ntp, inv_pos);
+    return hipGetLastError() == hipSuccess ? kOk : kErrHip;
+  }
   if (E <= 256)
     hipLaunchKernelGGL((moe_align_kernel<1024, 256>), dim3(1), dim3(1024), 0, stream, ids, numel, E, bm, P, sorted_ids,
                        expert_ids, ntp, inv_pos);

@@ -292,7 +292,9 @@ void w4o_moe_route(const float* logits, int64_t T, int64_t E, int64_t top_k, int
 /* sorted_ids has capacity P = T*k + (E+1)*(bm-1) (fused.py:94), pre-filled with the sentinel    */
 /* T*k; each expert's slots in increasing flat index order (stable), padded to a multiple of bm;  */
 /* expert_ids[b] = owning expert of block b, blocks past the end clamp to E-1; ntp = padded sum. */
-/* Returns P. inv_pos (optional, T*k) gets each slot's position in sorted_ids.                    */
+/* Returns P. inv_pos (optional, T*k) gets each slot's position in sorted_ids. Ids outside       */
+/* [0, E) (experts an expert-parallel rank does not hold) are dropped slots: not placed,         */
+/* inv_pos -1.                                                                                   */
 /* ------------------------------------------------------------------------------------------ */
 int64_t w4o_moe_align(const int32_t* ids, int64_t numel, int64_t E, int64_t bm, int32_t* sorted_ids,
                       int32_t* expert_ids, int32_t* ntp, int32_t* inv_pos) {
@@ -301,7 +303,8 @@ int64_t w4o_moe_align(const int32_t* ids, int64_t numel, int64_t E, int64_t bm, 
   int64_t* cnt = (int64_t*)calloc((size_t)E, sizeof(int64_t));
   int64_t* start = (int64_t*)calloc((size_t)E, sizeof(int64_t));
   int64_t* fill = (int64_t*)calloc((size_t)E, sizeof(int64_t));
-  for (int64_t i = 0; i < numel; ++i) cnt[ids[i]]++;
+  for (int64_t i = 0; i < numel; ++i)
+    if (ids[i] >= 0 && ids[i] < E) cnt[ids[i]]++;
   int64_t pos = 0;
   for (int64_t e = 0; e < E; ++e) {
     start[e] = pos;
@@ -310,6 +313,10 @@ int64_t w4o_moe_align(const int32_t* ids, int64_t numel, int64_t E, int64_t bm, 
   for (int64_t i = 0; i < P; ++i) sorted_ids[i] = (int32_t)numel;
   for (int64_t i = 0; i < numel; ++i) {
     int64_t e = ids[i];
+    if (e < 0 || e >= E) {
+      if (inv_pos) inv_pos[i] = -1;
+      continue;
+    }
     int64_t d = start[e] + fill[e]++;
     sorted_ids[d] = (int32_t)i;
     if (inv_pos) inv_pos[i] = (int32_t)d;

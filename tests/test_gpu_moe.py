@@ -97,6 +97,27 @@ def test_route_align_expert_counts(kernels, oracle, dev, E_, k, T):
     assert np.array_equal(expert_ids.cpu().numpy(), re_)
 
 
+@pytest.mark.parametrize("numel,E_,bm", [(4097, 128, 16), (32768, 128, 128), (70001, 128, 64), (20000, 300, 16),
+                                         (6000, 8, 128)])
+def test_moe_align_multi_workgroup_bit_exact(kernels, oracle, dev, numel, E_, bm):
+    """Above 4096 slots the align spans one workgroup per 1024 slots (512 for E > 256): sorted ids,
+    block owners, ntp and inverse positions equal the oracle's stable align bit for bit, with hot
+    experts and dropped ids (-1 and ids past E) in the route."""
+    g = np.random.default_rng(numel + E_)
+    ids = g.integers(0, E_, size=numel).astype(np.int32)
+    hot = g.random(numel) < 0.3
+    ids[hot] = g.integers(0, 3, size=int(hot.sum()))
+    drop = g.random(numel) < 0.05
+    ids[drop] = np.where(g.random(int(drop.sum())) < 0.5, -1, E_ + 7)
+    s, e, n, inv = kernels._moe_align(torch.from_numpy(ids).to(dev), E_, bm)
+    _sync()
+    rs, re_, rntp, rinv = oracle.moe_align(ids, E_, bm)
+    assert int(n.item()) == rntp
+    assert np.array_equal(s.cpu().numpy(), rs)
+    assert np.array_equal(e.cpu().numpy(), re_)
+    assert np.array_equal(inv.cpu().numpy()[:numel], rinv)
+
+
 def test_route_ties_keep_lower_index(kernels, dev):
     lg = torch.zeros(3, 16)
     lg[0] = torch.tensor([0.5, 1, 1, 1, -1, 1, 0, 2, 0, 0, 0, 0, 0, 0, 0, 0])

@@ -208,6 +208,22 @@ def test_moe_align_worked_example(oracle):
         assert sorted_ids[pos] == slot
 
 
+def test_moe_align_dropped_slots_are_an_extra_last_expert(oracle):
+    """Ids outside [0, E) are dropped: the layout of experts 0..E-1 equals that of the same route
+    with the dropped slots sent to an extra expert E (which sorts last), ntp ends where that extra
+    expert would start, and a dropped slot's inverse position is -1."""
+    rng = np.random.default_rng(5)
+    E, bm = 12, 16
+    ids = rng.integers(0, E, size=(300, 4)).astype(np.int32)
+    drop = rng.random(ids.shape) < 0.2
+    ids_d = np.where(drop, np.where(rng.random(ids.shape) < 0.5, -1, E + 3), ids).astype(np.int32)
+    s, e, ntp, inv = oracle.moe_align(ids_d, E, bm)
+    s2, e2, ntp2, inv2 = oracle.moe_align(np.where(drop, E, ids).astype(np.int32), E + 1, bm)
+    assert ntp < ntp2 and np.array_equal(s[:ntp], s2[:ntp]) and (s[ntp:] == ids.size).all()
+    assert np.array_equal(e[: ntp // bm], e2[: ntp // bm]) and (e[ntp // bm:] == E - 1).all()
+    assert np.array_equal(inv[~drop.ravel()], inv2[~drop.ravel()]) and (inv[drop.ravel()] == -1).all()
+
+
 def test_moe_align_matches_stable_sort(oracle):
     rng = np.random.default_rng(5)
     for T, E, k, bm in [(1, 128, 8, 16), (16, 128, 8, 16), (37, 16, 4, 32), (300, 128, 8, 64)]:
