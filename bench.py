@@ -213,6 +213,23 @@ def profile_prefill(kernels, dev, fmt: str, M: int, K: int, N: int) -> dict:
     return {"profile_prefill": fmt, "M": M, "K": K, "N": N, **_tflops(2.0 * M * N * K, us)}
 
 
+def profile_moe(kernels, dev, T: int) -> dict:
+    """One configs[4] MoE call shape (E=128, top-8, H=2048, I=768, int4 g128), 2 warm + 5 timed
+    calls, for kernel-trace and counter runs."""
+    import torch
+
+    gen = torch.Generator(device=dev).manual_seed(17)
+    E, k, H, I, g = 128, 8, 2048, 768, 128
+    w13 = kernels.repack_w4(_rand_words((E, 2 * I, H // 8), gen, dev))
+    s13 = (torch.randn(E, H // g, 2 * I, generator=gen, device=dev).abs() * 0.02 + 1e-4).to(torch.float16)
+    w2 = kernels.repack_w4(_rand_words((E, H, I // 8), gen, dev))
+    s2 = (torch.randn(E, I // g, H, generator=gen, device=dev).abs() * 0.02 + 1e-4).to(torch.float16)
+    x = make_x(T, H, 400 + T, dev)
+    logits = torch.randn(T, E, generator=gen, device=dev).to(torch.bfloat16)
+    us = _time_calls([lambda: kernels.w4a8_moe(x, w13, s13, None, w2, s2, None, logits, k, True)], 5)
+    return {"profile_moe": T, "us": round(us, 2)}
+
+
 def _time_calls(calls, reps: int) -> float:
     """Mean microseconds per call of `reps` calls cycling through `calls`, queued behind a GPU sleep
     and bracketed by one event pair on the launching stream (kernels plus back-to-back gaps)."""
@@ -439,6 +456,8 @@ def main() -> int:
     ap.add_argument("--no-configs", action="store_true")
     ap.add_argument("--profile-prefill", nargs=4, metavar=("FMT", "M", "K", "N"),
                     help="time one prefill GEMM (FMT int4, mxfp4 or nvfp4) and exit, for counter runs")
+    ap.add_argument("--profile-moe", type=int, metavar="T",
+                    help="time one configs[4] MoE call of T tokens and exit, for trace and counter runs")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -466,6 +485,9 @@ def main() -> int:
     if args.profile_kernel:
         r = roofline_leg(kernels, dev)
         print(json.dumps(r))
+        return 0
+    if args.profile_moe:
+        print(json.dumps(profile_moe(kernels, dev, args.profile_moe)))
         return 0
     if args.profile_prefill:
         f, m, k, n = args.profile_prefill
