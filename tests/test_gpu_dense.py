@@ -32,22 +32,27 @@ def _sync():
 
 
 def assert_close_to_oracle(got: torch.Tensor, ref: np.ndarray, what: str):
-    """Contract bar: rel L2 <= 2e-3 against the f64 oracle. Kernel bar: rel L2 <= 5e-4 against the
-    oracle rounded to the output dtype (REL_L2_ROUNDED). Structural guard: every element within
-    two output-dtype ulps plus 1e-4 of the output's magnitude (the MFMA's fp8 dot product
-    accumulates with slightly less than f32 precision, ~1e-5 relative, which shows up only where
-    outputs are small through cancellation)."""
+    """Contract bar: rel L2 <= 2e-3 against the f64 oracle; on small outputs, where the rounding of
+    the exact result to the output dtype alone can reach that (bf16 rounding is about 1.6e-3
+    relative L2 on average, more on a few hundred elements), the bar is that rounding's own
+    distance plus the kernel bar. Kernel bar: rel L2 <= 5e-4 against the oracle rounded to the
+    output dtype (REL_L2_ROUNDED). Structural guard: every element within two output-dtype ulps
+    plus 1e-4 of the output's magnitude (the MFMA's fp8 dot product accumulates with slightly less
+    than f32 precision, ~1e-5 relative, which shows up only where outputs are small through
+    cancellation)."""
     g = got.float().cpu().numpy().astype(np.float64)
-    rel = np.linalg.norm(g - ref) / max(np.linalg.norm(ref), 1e-30)
+    nref = max(np.linalg.norm(ref), 1e-30)
+    rel = np.linalg.norm(g - ref) / nref
     dt = torch.bfloat16 if got.dtype == torch.bfloat16 else torch.float16
     rounded = torch.from_numpy(ref).to(dt).double().numpy()
-    rel_r = np.linalg.norm(g - rounded) / max(np.linalg.norm(ref), 1e-30)
+    rel_r = np.linalg.norm(g - rounded) / nref
+    bar = max(REL_L2, np.linalg.norm(rounded - ref) / nref + REL_L2_ROUNDED)
     ulp_bits = 7 if got.dtype == torch.bfloat16 else 10
     tol = 2 * np.abs(ref) * 2.0 ** -ulp_bits + 1e-4 * np.abs(ref).max()
     bad = np.abs(g - ref) > tol
     print(f"[parity] {what}: rel L2 {rel:.3e} (vs dtype-rounded oracle {rel_r:.3e}), outliers {int(bad.sum())}",
           flush=True)
-    assert rel <= REL_L2, f"{what}: rel L2 {rel:.3e} > {REL_L2}"
+    assert rel <= bar, f"{what}: rel L2 {rel:.3e} > {bar:.3e}"
     assert rel_r <= REL_L2_ROUNDED, f"{what}: rel L2 vs the dtype-rounded oracle {rel_r:.3e} > {REL_L2_ROUNDED}"
     assert not bad.any(), f"{what}: {bad.sum()} elements off, worst {np.abs(g - ref)[bad].max():.3e}"
     return rel
@@ -332,3 +337,45 @@ def test_dispatch_ledger_records_arms(kernels, dev):
     _sync()
     d = eng.counts_delta(before)
     assert d.get("w4a8_mi355x.gemm(decode_gemv)") == 1 and d.get("w4a8_mi355x.gemm(wmma_tiled_tuned)") == 1
+
+
+# ------------------------------------------------------------------------------- edge shapes
+@pytest.mark.parametrize("fmt,g", [("sym", 32), ("asym", 64), ("mxfp4", 32), ("nvfp4", 16)])
+@pytest.mark.parametrize("M,K,N", [(17, 160, 16), (40, 2592, 48), (300, 1088, 144), (5, 96, 32)])
+def test_edge_shapes(kernels, oracle, dev, fmt, g, M, K, N):
+    """K that is not a multiple of 128 (the tile's zero padding, the per-wave prefill kernel), one
+    strip (N=16), row counts on both arms, every weight format; against the oracle."""
+    if K % g:
+        pytest.skip("group does not divide K")
+    if fmt in ("sym", "asym"):
+        w, s, z = synth.int4_weight(N, K, g, seed=M + K, asym=fmt == "asym", scale_floor=1e-4)
+        e2, nv = False, False
+    elif fmt == "mxfp4":
+        w, s = synth.mxfp4_weight(N, K, seed=M + K)
+        z, e2, nv = None, True, False
+    else:
+        w, s, z = synth.nvfp4_weight(N, K, seed=M + K)
+        e2, nv = True, True
+    x = synth.activations(M, K, seed=M)
+    xq, xs = oracle.act_quant(synth.bits16(x), 0)
+    sv = s.view(torch.uint8).numpy() if nv else s.numpy()
+    ref = oracle.gemm(xq, xs, w.numpy(), sv, None if z is None else z.numpy(), g, e2, nv)
+    tiles = kernels.repack_w4(w.to(dev), weight_is_e2m1=e2)
+    out = kernels.w4a8_linear(x.to(dev), tiles, s.to(dev), None if z is None else z.to(dev), g, weight_is_e2m1=e2)
+    _sync()
+    assert tuple(out.shape) == (M, N)
+    assert_close_to_oracle(out, ref, f"{fmt} g={g} M={M} K={K} N={N}")
+
+
+def test_empty_batch(kernels, dev):
+    """M = 0 returns an empty (0, N) result on both arms and the fused silu arm, without a launch
+    error."""
+    K, N, g = 512, 64, 128
+    w, s, _ = synth.int4_weight(N, K, g, seed=3, asym=False)
+    tiles, sd = kernels.repack_w4(w.to(dev)), s.to(dev)
+    x = torch.empty((0, K), dtype=torch.bfloat16, device=dev)
+    for kern in (None, "decode_gemv", "wmma_tiled_tuned"):
+        out = kernels.w4a8_linear(x, tiles, sd, None, g, kernel=kern)
+        assert tuple(out.shape) == (0, N)
+    assert tuple(kernels.w4a8_linear_silu(x, tiles, sd, None, g).shape) == (0, N // 2)
+    _sync()

@@ -496,3 +496,26 @@ def test_w4a16_moe_silu_split_refusals(kernels, dev):
     assert lib.w4a16_moe_silu_split(p(y), 64, p(inv), 2, 2, 32, 5, p(q), 32, p(s), None, 0, st) == 1  # dtype
     assert lib.w4a16_moe_silu_split(p(y), 64, p(inv), 2, 2, 32, 1, p(q), 32, None, None, 0, st) == 1  # scales
     assert b"silu_split" in lib.w4a8_last_error()
+
+
+@pytest.mark.parametrize("E_,k,T", [(1, 1, 5), (4, 4, 7), (8, 1, 33), (16, 2, 300)])
+def test_moe_edge_routes(kernels, oracle, dev, E_, k, T):
+    """A single expert, top_k = E (every expert for every token), top_k = 1, and a batch on the
+    MFMA arm: end to end against the oracle's f64 forward within what the stages account for."""
+    h, i = 256, 128
+    w13, s13, _ = synth.int4_weight(2 * i, h, G, seed=600 + E_, asym=False, E=E_, scale_floor=1e-3)
+    w2, s2, _ = synth.int4_weight(h, i, G, seed=601 + E_, asym=False, E=E_, scale_floor=1e-3)
+    x = synth.activations(T, h, seed=602 + T)
+    lg = synth.router_logits(T, E_, seed=603 + T)
+    res = kernels._moe_forward(x.to(dev), w13.to(dev), s13.to(dev), None, w2.to(dev), s2.to(dev), None, lg.to(dev),
+                               k, True)
+    _sync()
+    rows = _subset(T)
+    rel1, rel2, y2ref = _stagewise(kernels, oracle, res, x, w13, s13, None, w2, s2, None, rows)
+    assert rel1 <= 2e-3 and rel2 <= 2e-3
+    tw, ids = oracle.moe_route(lg.float().numpy(), k, True)
+    sub = torch.tensor(rows)
+    sorted_ids, expert_ids, ntp, _ = oracle.moe_align(ids[rows], E_, 16)
+    ref = oracle.moe_forward(synth.bits16(x[sub]), 0, tw[rows], sorted_ids, expert_ids, ntp, 16, k, w13.numpy(),
+                             s13.numpy(), None, w2.numpy(), s2.numpy(), None)
+    _assert_end_to_end(res["out"][sub.to(dev)], ref, y2ref, rel2, f"moe E={E_} k={k} T={T}")
