@@ -13,9 +13,10 @@
 //   operand) and writes it to LDS, with its fp16 scales and zero words.
 // Each stage is its own __shared__ array and every stage index is a compile-time constant (the K
 // loop is unrolled by three), so the compiler tells the stages apart: reading stage k does not
-// wait for the DMAs in flight to stages k+1 and k+2. Step k issues the loads of step k+2, computes
-// step k, writes the int4 registers of step k+1, then waits for its own step-k+1 loads (a counted
-// vmcnt, the loads of step k+2 stay in flight) and meets the other waves at one s_barrier.
+// wait for the DMAs in flight to stages k+1 and k+2. Step k issues the loads of step k+2 (int4:
+// between its MFMAs), computes step k, writes the int4 registers of step k+1, then waits for its
+// own step-k+1 loads (a counted vmcnt, the loads of step k+2 stay in flight) and meets the other
+// waves at one s_barrier.
 #include <cstdlib>
 
 #include "prefill.h"
@@ -145,7 +146,8 @@ gemm_dma_kernel(const GemmArgs p) {
   uint2 rzp[3];
 
   // loads of K step kt into stage I (DMA) / register set I (int4 weights, scales, zeros)
-  auto issue = [&](auto I, int kt) __attribute__((always_inline)) {
+  // part: 1 = the A DMAs (and fp4 strips / E8M0 bytes), 2 = the int4 weight, scale and zero loads
+  auto issue = [&](auto I, int kt, int part = 3) __attribute__((always_inline)) {
     constexpr int R = decltype(I)::value;
     unsigned char* st = stage(I);
     if constexpr (kFp4) {
@@ -155,15 +157,17 @@ gemm_dma_kernel(const GemmArgs p) {
                  (uint32_t)__builtin_amdgcn_readfirstlane(kt * 4 * N));
     }
     const uint32_t so_a = (uint32_t)__builtin_amdgcn_readfirstlane(kt * kTileK);
+    if (part & 1) {
 #pragma unroll
-    for (int i = 0; i < A_PER; ++i)
-      lds_dma16(rs_a, st + (wave + i * NW) * 1024, a_voff[i], so_a);
+      for (int i = 0; i < A_PER; ++i)
+        lds_dma16(rs_a, st + (wave + i * NW) * 1024, a_voff[i], so_a);
+    }
     if constexpr (kFp4) {
 #pragma unroll
       for (int i = 0; i < B_DMA; ++i)
         lds_dma16(rs_w, st + S::kA + (wave + i * NW) * 1024, (uint32_t)lane * 16,
                     (uint32_t)__builtin_amdgcn_readfirstlane((b_gs[i] * KT + kt) * kTileBytes));
-    } else {
+    } else if (part & 2) {
       const uint32_t so_b = (uint32_t)__builtin_amdgcn_readfirstlane(kt * kTileBytes);
 #pragma unroll
       for (int i = 0; i < B_PER; ++i) rbw[R][i] = bload128v(rs_w, b_voff[i], so_b);
@@ -208,8 +212,8 @@ gemm_dma_kernel(const GemmArgs p) {
   const int zsh = 4 * (lane & 7);
 
   // MFMA work of one K step from stage I (operands read one row block / strip ahead of their
-  // MFMAs). int4: mid() runs right after the first strip's MFMAs are issued, so its VALU work
-  // (the unpack of the next step's weights) overlaps MFMAs in flight.
+  // MFMAs). int4: mid(j) runs right after strip j's MFMAs are issued (j = 0, 1), so its work (the
+  // loads of a later step, the unpack of the next step's weights) overlaps MFMAs in flight.
   auto compute = [&](auto I, auto mid) __attribute__((always_inline)) {
     const unsigned char* st = stage(I);
     if constexpr (kFp4) {
@@ -259,7 +263,7 @@ gemm_dma_kernel(const GemmArgs p) {
           __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
           for (int rb = 0; rb < RB; ++rb) cj[rb] = mfma_f8f8(a[rb], b, MODE == kPSym ? pre[rb] : zero4);
-          if (j == 0) mid();
+          if (j < 2) mid(j);
         }
         if (j > 0) {
 #pragma unroll
@@ -292,12 +296,27 @@ gemm_dma_kernel(const GemmArgs p) {
   };
 
   // one pipelined step kt (stage C = kt % 3): loads of kt+2, MFMAs of kt, int4 registers of kt+1
-  // to LDS, wait for kt+1's loads, barrier
+  // to LDS, wait for kt+1's loads, barrier. int4 issues kt+2's loads between its MFMAs (the A DMAs
+  // after the first strip's, the weight loads after the second's) instead of ahead of them all: at
+  // the top of the step every wave's loads would meet in the address unit's queue while the step's
+  // first MFMAs wait (1-4% on configs[3] shapes).
   auto step = [&](auto C, int kt) __attribute__((always_inline)) {
     constexpr int c = decltype(C)::value, n1 = (c + 1) % 3, n2 = (c + 2) % 3;
-    issue(IC<n2>{}, kt + 2);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(C, [&]() __attribute__((always_inline)) { commit(IC<n1>{}, IC<n1>{}); });
+    static_assert(kFp4 || NSB >= 2, "int4 steps issue their loads after strips 0 and 1");
+    if constexpr (kFp4) {
+      issue(IC<n2>{}, kt + 2);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(C, [&](int) __attribute__((always_inline)) {});
+    } else {
+      compute(C, [&](int j) __attribute__((always_inline)) {
+        if (j == 0) {
+          issue(IC<n2>{}, kt + 2, 1);
+          commit(IC<n1>{}, IC<n1>{});
+        } else {
+          issue(IC<n2>{}, kt + 2, 2);
+        }
+      });
+    }
     __builtin_amdgcn_sched_barrier(0);
     wait_vm_lgkm0<NOPS>();
     __builtin_amdgcn_s_barrier();
@@ -308,8 +327,8 @@ gemm_dma_kernel(const GemmArgs p) {
     if (kt >= KT) return;
     const bool more = kt + 2 < KT;
     if (more) issue(IC<n2>{}, kt + 2);
-    compute(C, [&]() __attribute__((always_inline)) {
-      if (kt + 1 < KT) commit(IC<n1>{}, IC<n1>{});
+    compute(C, [&](int j) __attribute__((always_inline)) {
+      if (j == 0 && kt + 1 < KT) commit(IC<n1>{}, IC<n1>{});
     });
     if (more) wait_vm_lgkm0<NOPS>();
     else wait_vm_lgkm0<0>();
