@@ -212,8 +212,9 @@ gemm_dma_kernel(const GemmArgs p) {
   const int zsh = 4 * (lane & 7);
 
   // MFMA work of one K step from stage I (operands read one row block / strip ahead of their
-  // MFMAs). int4: mid(j) runs right after strip j's MFMAs are issued (j = 0, 1), so its work (the
-  // loads of a later step, the unpack of the next step's weights) overlaps MFMAs in flight.
+  // MFMAs). mid(i) runs right after the MFMAs of int4 strip i (i = 0, 1) or MXFP4 row block i, so
+  // its work (the loads of a later step, the unpack of the next step's weights) overlaps MFMAs in
+  // flight.
   auto compute = [&](auto I, auto mid) __attribute__((always_inline)) {
     const unsigned char* st = stage(I);
     if constexpr (kFp4) {
@@ -232,6 +233,7 @@ gemm_dma_kernel(const GemmArgs p) {
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int j = 0; j < NSB; ++j) acc[rb][j] = mfma_f8f4_sb(a0, fp4_operand(braw[j]), acc[rb][j], sbyte[j]);
+        mid(rb);
         if (rb + 1 < RB) a0 = a1;
       }
     } else {
@@ -296,17 +298,18 @@ gemm_dma_kernel(const GemmArgs p) {
   };
 
   // one pipelined step kt (stage C = kt % 3): loads of kt+2, MFMAs of kt, int4 registers of kt+1
-  // to LDS, wait for kt+1's loads, barrier. int4 issues kt+2's loads between its MFMAs (the A DMAs
-  // after the first strip's, the weight loads after the second's) instead of ahead of them all: at
-  // the top of the step every wave's loads would meet in the address unit's queue while the step's
-  // first MFMAs wait (1-4% on configs[3] shapes).
+  // to LDS, wait for kt+1's loads, barrier. The loads of kt+2 are issued between the step's MFMAs
+  // instead of ahead of them all (int4: the A DMAs after the first strip's, the weight loads after
+  // the second's; MXFP4: all after the second row block's): at the top of the step every wave's
+  // loads would meet in the address unit's queue while the step's first MFMAs wait (1-4% on
+  // configs[3] and configs[5] shapes).
   auto step = [&](auto C, int kt) __attribute__((always_inline)) {
     constexpr int c = decltype(C)::value, n1 = (c + 1) % 3, n2 = (c + 2) % 3;
     static_assert(kFp4 || NSB >= 2, "int4 steps issue their loads after strips 0 and 1");
     if constexpr (kFp4) {
-      issue(IC<n2>{}, kt + 2);
-      __builtin_amdgcn_sched_barrier(0);
-      compute(C, [&](int) __attribute__((always_inline)) {});
+      compute(C, [&](int rb) __attribute__((always_inline)) {
+        if (rb == 1) issue(IC<n2>{}, kt + 2);
+      });
     } else {
       compute(C, [&](int j) __attribute__((always_inline)) {
         if (j == 0) {
