@@ -207,8 +207,8 @@ gemm_nv_kernel(const GemmArgs p) {
   asm volatile("" : "+v"(oa), "+v"(ob));
 
   // the four fp16 sub-steps of a K step from A stage I and B stage BI (each sub-step's B fragments
-  // read one sub-step ahead of its MFMAs); mid() runs after the first sub-step's MFMAs are issued
-  // (the next step's B decode overlaps them)
+  // read one sub-step ahead of its MFMAs); mid(s) runs after sub-step s's MFMAs are issued (the
+  // next step's B decode and later loads overlap them)
   auto compute = [&](auto I, auto BI, auto mid) __attribute__((always_inline)) {
     const unsigned char* sa = astage(I);
     const unsigned char* bs = bstage(BI);
@@ -237,7 +237,7 @@ gemm_nv_kernel(const GemmArgs p) {
       for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
         for (int j = 0; j < NSB; ++j) acc[rb][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[rb], bc[j], acc[rb][j], 0, 0, 0);
-      if (s == 0) mid();
+      mid(s);
       if (s < 3) {
 #pragma unroll
         for (int j = 0; j < NSB; ++j) bc[j] = bn[j];
@@ -245,13 +245,16 @@ gemm_nv_kernel(const GemmArgs p) {
     }
   };
 
-  // one pipelined step kt (A stage C = kt % 3, B stage D = kt % 2): loads of kt+2, MFMAs of kt,
-  // B registers of kt+1 to LDS, wait for kt+1's loads, barrier
+  // one pipelined step kt (A stage C = kt % 3, B stage D = kt % 2): MFMAs of kt, B registers of
+  // kt+1 to LDS (after the first sub-step's MFMAs), loads of kt+2 (after the second's, rather than
+  // ahead of all of them, where every wave's loads would meet in the address unit's queue while the
+  // first MFMAs wait: 4-6% at M=4096), wait for kt+1's loads, barrier
   auto step = [&](auto C, auto D, int kt) __attribute__((always_inline)) {
     constexpr int c = decltype(C)::value, d = decltype(D)::value, n1 = (c + 1) % 3, n2 = (c + 2) % 3;
-    issue(IC<n2>{}, kt + 2);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(C, D, [&]() __attribute__((always_inline)) { commit(IC<n1>{}, IC<1 - d>{}); });
+    compute(C, D, [&](int s) __attribute__((always_inline)) {
+      if (s == 0) commit(IC<n1>{}, IC<1 - d>{});
+      if (s == 1) issue(IC<n2>{}, kt + 2);
+    });
     __builtin_amdgcn_sched_barrier(0);
     wait_vm_lgkm0<NOPS>();
     __builtin_amdgcn_s_barrier();
@@ -262,8 +265,8 @@ gemm_nv_kernel(const GemmArgs p) {
     if (kt >= KT) return;
     const bool more = kt + 2 < KT;
     if (more) issue(IC<n2>{}, kt + 2);
-    compute(C, D, [&]() __attribute__((always_inline)) {
-      if (kt + 1 < KT) commit(IC<n1>{}, IC<1 - d>{});
+    compute(C, D, [&](int s) __attribute__((always_inline)) {
+      if (s == 0 && kt + 1 < KT) commit(IC<n1>{}, IC<1 - d>{});
     });
     if (more) wait_vm_lgkm0<NOPS>();
     else wait_vm_lgkm0<0>();
