@@ -386,6 +386,90 @@ moe_align_kernel(const int32_t* __restrict__ ids, int64_t numel, int E, int bm, 
 // tokens (one wave per token, 16 at a time), keeping the ids in LDS, then aligns them; workgroups
 // 1..T each quantize one token row of x (quant_row, the act-quant kernel's arithmetic) in parallel
 // with it.
+// Align of at most 64 slots (the decode batches of the prep launch): one wave counts, scans and
+// places the slots with no LDS barrier, then (align_fill, after one barrier) the workgroup writes
+// the padding sentinels, the tail and the block owners. Lane l owns experts l + 64k (k < EPL) for
+// the counts and the scan, and slot l for the scatter; a slot's position is its expert's start plus
+// the number of earlier slots of that expert, so every output equals align_block's. ids in LDS;
+// base_s, cnt_s, total_s: LDS for the expert starts, the counts and ntp. Measured against
+// align_block in the prep launch: T=1 7.9 -> 6.9 us, T=4 7.9 -> 7.6 us (the fills were a third of
+// the launch when one wave wrote them).
+template <int EPL>
+__device__ __forceinline__ void align_wave(const int32_t* ids, int numel, int E, int bm, int64_t P,
+                                           int32_t* __restrict__ sorted_ids, int32_t* __restrict__ expert_ids,
+                                           int32_t* __restrict__ ntp_out, int32_t* __restrict__ inv_pos, int* base_s,
+                                           int* cnt_s, int* total_s) {
+  const int lane = threadIdx.x & 63;
+  int cnt[EPL];
+#pragma unroll
+  for (int k = 0; k < EPL; ++k) cnt[k] = 0;
+  for (int i = 0; i < numel; ++i) {
+    const int e = ids[i];
+#pragma unroll
+    for (int k = 0; k < EPL; ++k) cnt[k] += e == lane + 64 * k ? 1 : 0;
+  }
+  // exclusive scan of the padded counts over experts in order
+  int base[EPL], padded[EPL];
+  int run = 0;
+#pragma unroll
+  for (int k = 0; k < EPL; ++k) {
+    const int e = lane + 64 * k;
+    padded[k] = e < E ? (cnt[k] + bm - 1) / bm * bm : 0;
+    int incl = padded[k];
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int n = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += n;
+    }
+    base[k] = run + incl - padded[k];
+    run += __shfl(incl, 63, 64);
+    if (e < E) base_s[e] = base[k];
+  }
+  const int total = run;
+  // the wave's LDS writes above are complete before its reads below (one wave, in order)
+  if (lane < numel) {
+    const int e = ids[lane];
+    if (e >= 0 && e < E) {
+      int rank = 0;
+      for (int j = 0; j < lane; ++j) rank += ids[j] == e ? 1 : 0;
+      const int off = base_s[e] + rank;
+      sorted_ids[off] = lane;
+      if (inv_pos) inv_pos[lane] = off;
+    } else if (inv_pos) {
+      inv_pos[lane] = -1;  // dropped slot: the combine skips it
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < EPL; ++k)
+    if (lane + 64 * k < E) cnt_s[lane + 64 * k] = cnt[k];
+  if (lane == 0) {
+    *ntp_out = total;
+    *total_s = total;
+  }
+}
+
+// The rest of the align after align_wave, spread over the NT threads of the workgroup (after a
+// barrier): padding rows of each expert, the tail [total, P) and the block owners.
+template <int NT>
+__device__ __forceinline__ void align_fill(int numel, int E, int bm, int64_t P, int32_t* __restrict__ sorted_ids,
+                                           int32_t* __restrict__ expert_ids, const int* base_s, const int* cnt_s,
+                                           int total) {
+  const int tid = threadIdx.x;
+  const int pad = bm - 1;
+  for (int x = tid; x < E * pad; x += NT) {
+    const int e = x / pad, j = x - e * pad;
+    const int c = cnt_s[e];
+    if (c + j < (c + bm - 1) / bm * bm) sorted_ids[base_s[e] + c + j] = numel;
+  }
+  for (int e = tid; e < E; e += NT) {
+    const int nb = (cnt_s[e] + bm - 1) / bm, b0 = base_s[e] / bm;
+    for (int b = 0; b < nb; ++b) expert_ids[b0 + b] = e;
+  }
+  for (int i = total + tid; i < (int)P; i += NT) sorted_ids[i] = numel;
+  const int nblocks = (int)((P + bm - 1) / bm);
+  for (int b = total / bm + tid; b < nblocks; b += NT) expert_ids[b] = E - 1;
+}
+
 constexpr int kPrepThreads = 1024;
 constexpr int kPrepMaxSlots = 256;
 
@@ -406,6 +490,15 @@ moe_prep_kernel(const void* __restrict__ logits, int ldtype, int64_t T, int E, i
   for (int64_t t = threadIdx.x >> 6; t < T; t += kPrepThreads / 64)
     route_token<PER>(logits, ldtype, t, E, top_k, renorm, tw, ids, ids_s);
   lds_barrier();
+  if (T * top_k <= 64) {
+    // decode batches: one wave counts, scans and places the slots, then the workgroup fills
+    __shared__ int base_s[64 * PER], cnt_s[64 * PER], total_s;
+    if (threadIdx.x < 64)
+      align_wave<PER>(ids_s, (int)(T * top_k), E, bm, P, sorted_ids, expert_ids, ntp, inv_pos, base_s, cnt_s, &total_s);
+    lds_barrier();
+    align_fill<kPrepThreads>((int)(T * top_k), E, bm, P, sorted_ids, expert_ids, base_s, cnt_s, total_s);
+    return;
+  }
   align_block<kPrepThreads, 64 * PER, 0>(ids_s, T * top_k, E, bm, P, sorted_ids, expert_ids, ntp, inv_pos);
 }
 
