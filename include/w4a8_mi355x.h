@@ -123,6 +123,20 @@ int w4a8_moe_route_align(const void* logits, int logits_dtype, int64_t T, int64_
                          int32_t* expert_ids, int32_t* ntp, int32_t* inv_pos, const void* x, int x_dtype, int64_t K,
                          int64_t ldx, uint8_t* x_fp8, int64_t ldq, float* x_scales, void* stream);
 
+/* Route (+ the per-token quant of x) as w4a8_moe_route_align, but instead of the align every slot gets a
+ * block of its own: slot s's padded row is s*block_m, the block's other rows are sentinels
+ * (T*top_k), expert_ids[s] is its expert, inv_pos[s] = s*block_m, ntp = T*top_k*block_m. Only
+ * [0, ntp) of sorted_ids and the first T*top_k blocks of expert_ids are written. No counterpart in
+ * the reference: w4a8_moe uses it for calls of up to 8 tokens on the decode arm (a token's experts
+ * are distinct, and a few tokens share few), where the align's sort and its padding fills are a
+ * third of the routing launch and the grouped GEMMs read no row past ntp. Needs T*top_k <= 256,
+ * T*top_k <= E (the grouped GEMMs size their grids for numel/block_m + min(E, numel) blocks),
+ * T*top_k*block_m <= P and inv_pos. */
+int w4a8_moe_route_slots(const void* logits, int logits_dtype, int64_t T, int64_t E, int top_k, int renormalize,
+                         int block_m, int64_t P, float* topk_w, int32_t* topk_ids, int32_t* sorted_ids,
+                         int32_t* expert_ids, int32_t* ntp, int32_t* inv_pos, const void* x, int x_dtype, int64_t K,
+                         int64_t ldx, uint8_t* x_fp8, int64_t ldq, float* x_scales, void* stream);
+
 /* RMSNorm producer with the per-token fp8 quant of its output as an epilogue. Replaces tail_hip's
  * rms_norm / rms_norm_add / rms_norm_quant / rms_norm_add_quant (python/minisgl/layers/norm.py:9-58,
  * 134-168): with residual non-NULL, residual <- x + residual (in place, in the activation dtype) and

@@ -43,6 +43,8 @@ SIGNATURES = {
                                _c_i64, _vp, _c_i64, _vp, _vp]),
     "w4a8_moe_route_align": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_i64, _vp, _vp, _vp,
                                       _vp, _vp, _vp, _vp, _c_int, _c_i64, _c_i64, _vp, _c_i64, _vp, _vp]),
+    "w4a8_moe_route_slots": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_i64, _vp, _vp, _vp,
+                                      _vp, _vp, _vp, _vp, _c_int, _c_i64, _c_i64, _vp, _c_i64, _vp, _vp]),
     "w4a8_moe_padded_capacity": (_c_i64, [_c_i64, _c_i64, _c_int]),
     "w4a8_moe_align": (_c_int, [_vp, _c_i64, _c_i64, _c_int, _c_i64, _vp, _vp, _vp, _vp, _vp]),
     "w4a8_moe_gemm_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_int, _c_i64, _c_i64, _c_i64, _c_int]),

@@ -41,7 +41,7 @@ int launch_moe_silu_split(const float* y, int64_t ldy, const int32_t* inv_pos, i
 int launch_moe_prep(const void* logits, int ldtype, int64_t T, int E, int top_k, int renorm, float* tw,
                     int32_t* ids, int bm, int64_t P, int32_t* sorted_ids, int32_t* expert_ids, int32_t* ntp,
                     int32_t* inv_pos, const void* x, int xdtype, int64_t K, int64_t ldx, uint8_t* xq, int64_t ldq,
-                    float* xs, hipStream_t stream);
+                    float* xs, int slots, hipStream_t stream);
 }  // namespace w4a8
 
 using namespace w4a8;
@@ -366,6 +366,19 @@ int w4a8_moe_route(const void* logits, int logits_dtype, int64_t T, int64_t E, i
                                      (hipStream_t)stream), "moe_route");
 }
 
+static int check_route_x(const char* what, const void* x, int x_dtype, int64_t K, int64_t ldx, const void* x_fp8,
+                         int64_t ldq, const float* x_scales) {
+  if (!x) return kOk;
+  if (x_dtype != kBF16 && x_dtype != kF16) return fail(kErrInvalid, "%s: x must be bf16 or fp16", what);
+  if (K <= 0 || K % 8) return fail(kErrInvalid, "%s: K=%lld must be a positive multiple of 8", what, (long long)K);
+  if (ldx < K || ldx % 8 || ldq < K || ldq % 8)
+    return fail(kErrInvalid, "%s: row strides must be >= K and multiples of 8 (ldx=%lld ldq=%lld)", what,
+                (long long)ldx, (long long)ldq);
+  if (!aligned16(x) || !aligned16(x_fp8) || !x_scales)
+    return fail(kErrInvalid, "%s: x and x_fp8 must be 16-byte aligned and x_scales given", what);
+  return kOk;
+}
+
 int w4a8_moe_route_align(const void* logits, int logits_dtype, int64_t T, int64_t E, int top_k, int renormalize,
                          int block_m, int64_t P, float* topk_w, int32_t* topk_ids, int32_t* sorted_ids,
                          int32_t* expert_ids, int32_t* ntp, int32_t* inv_pos, const void* x, int x_dtype, int64_t K,
@@ -373,24 +386,34 @@ int w4a8_moe_route_align(const void* logits, int logits_dtype, int64_t T, int64_
   if (int rc = check_route("moe_route_align", logits_dtype, E, top_k)) return rc;
   if (T < 0) return fail(kErrInvalid, "moe_route_align: T=%lld negative", (long long)T);
   if (int rc = check_align("moe_route_align", T * top_k, E, block_m, P)) return rc;
-  if (x) {
-    if (x_dtype != kBF16 && x_dtype != kF16) return fail(kErrInvalid, "moe_route_align: x must be bf16 or fp16");
-    if (K <= 0 || K % 8) return fail(kErrInvalid, "moe_route_align: K=%lld must be a positive multiple of 8", (long long)K);
-    if (ldx < K || ldx % 8 || ldq < K || ldq % 8)
-      return fail(kErrInvalid, "moe_route_align: row strides must be >= K and multiples of 8 (ldx=%lld ldq=%lld)",
-                  (long long)ldx, (long long)ldq);
-    if (!aligned16(x) || !aligned16(x_fp8) || !x_scales)
-      return fail(kErrInvalid, "moe_route_align: x and x_fp8 must be 16-byte aligned and x_scales given");
-  }
+  if (int rc = check_route_x("moe_route_align", x, x_dtype, K, ldx, x_fp8, ldq, x_scales)) return rc;
   const hipStream_t st = (hipStream_t)stream;
   if (moe_prep_fits(T, top_k))
     return hip_status(launch_moe_prep(logits, logits_dtype, T, (int)E, top_k, renormalize, topk_w, topk_ids, block_m, P,
                                       sorted_ids, expert_ids, ntp, inv_pos, x, x_dtype, K, ldx, x_fp8, ldq, x_scales,
-                                      st), "moe_route_align");
+                                      0, st), "moe_route_align");
   int rc = launch_moe_route(logits, logits_dtype, T, (int)E, top_k, renormalize, topk_w, topk_ids, st);
   if (!rc) rc = launch_moe_align(topk_ids, T * top_k, (int)E, block_m, P, sorted_ids, expert_ids, ntp, inv_pos, st);
   if (!rc && x) rc = launch_act_quant(x, x_dtype, T, K, ldx, x_fp8, ldq, x_scales, nullptr, st);
   return hip_status(rc, "moe_route_align");
+}
+
+int w4a8_moe_route_slots(const void* logits, int logits_dtype, int64_t T, int64_t E, int top_k, int renormalize,
+                         int block_m, int64_t P, float* topk_w, int32_t* topk_ids, int32_t* sorted_ids,
+                         int32_t* expert_ids, int32_t* ntp, int32_t* inv_pos, const void* x, int x_dtype, int64_t K,
+                         int64_t ldx, uint8_t* x_fp8, int64_t ldq, float* x_scales, void* stream) {
+  if (int rc = check_route("moe_route_slots", logits_dtype, E, top_k)) return rc;
+  if (T < 0) return fail(kErrInvalid, "moe_route_slots: T=%lld negative", (long long)T);
+  if (int rc = check_align("moe_route_slots", T * top_k, E, block_m, P)) return rc;
+  if (int rc = check_route_x("moe_route_slots", x, x_dtype, K, ldx, x_fp8, ldq, x_scales)) return rc;
+  // the grouped GEMMs size their grids for numel / block_m + min(E, numel) blocks: no more slots
+  // than experts
+  if (!moe_prep_fits(T, top_k) || T * top_k * block_m > P || T * top_k > E || !inv_pos)
+    return fail(kErrInvalid, "moe_route_slots: T*top_k=%lld slots of %d rows must fit P=%lld, E=%lld and the "
+                "one-launch prep, with inv_pos given", (long long)(T * top_k), block_m, (long long)P, (long long)E);
+  return hip_status(launch_moe_prep(logits, logits_dtype, T, (int)E, top_k, renormalize, topk_w, topk_ids, block_m, P,
+                                    sorted_ids, expert_ids, ntp, inv_pos, x, x_dtype, K, ldx, x_fp8, ldq, x_scales, 1,
+                                    (hipStream_t)stream), "moe_route_slots");
 }
 
 int64_t w4a8_moe_padded_capacity(int64_t numel, int64_t E, int block_m) {

@@ -473,13 +473,17 @@ __device__ __forceinline__ void align_fill(int numel, int E, int bm, int64_t P, 
 constexpr int kPrepThreads = 1024;
 constexpr int kPrepMaxSlots = 256;
 
+// slots: instead of the align, give every slot a block of its own (slot s: padded row s*bm, the
+// block's other rows sentinels, block owner its expert; ntp = slots * bm). Only [0, ntp) of
+// sorted_ids and the first `slots` blocks of expert_ids are written: the grouped GEMMs read no row
+// at or past ntp, and the combine reads inv_pos.
 template <int PER, int CPT>
 __global__ void __launch_bounds__(kPrepThreads)
 moe_prep_kernel(const void* __restrict__ logits, int ldtype, int64_t T, int E, int top_k, int renorm,
                 float* __restrict__ tw, int32_t* __restrict__ ids, int bm, int64_t P,
                 int32_t* __restrict__ sorted_ids, int32_t* __restrict__ expert_ids, int32_t* __restrict__ ntp,
                 int32_t* __restrict__ inv_pos, const uint16_t* __restrict__ x, int xdtype, int64_t K, int64_t ldx,
-                uint8_t* __restrict__ xq, int64_t ldq, float* __restrict__ xs) {
+                uint8_t* __restrict__ xq, int64_t ldq, float* __restrict__ xs, int slots) {
   if (blockIdx.x > 0) {
     __shared__ float red[kPrepThreads / 64];
     const int64_t m = blockIdx.x - 1;
@@ -490,6 +494,16 @@ moe_prep_kernel(const void* __restrict__ logits, int ldtype, int64_t T, int E, i
   for (int64_t t = threadIdx.x >> 6; t < T; t += kPrepThreads / 64)
     route_token<PER>(logits, ldtype, t, E, top_k, renorm, tw, ids, ids_s);
   lds_barrier();
+  if (slots) {
+    const int S = (int)(T * top_k);
+    for (int i = threadIdx.x; i < S * bm; i += kPrepThreads) sorted_ids[i] = i % bm == 0 ? i / bm : S;
+    if (threadIdx.x < S) {
+      expert_ids[threadIdx.x] = ids_s[threadIdx.x];
+      inv_pos[threadIdx.x] = (int32_t)threadIdx.x * bm;
+    }
+    if (threadIdx.x == 0) *ntp = S * bm;
+    return;
+  }
   if (T * top_k <= 64) {
     // decode batches: one wave counts, scans and places the slots, then the workgroup fills
     __shared__ int base_s[64 * PER], cnt_s[64 * PER], total_s;
@@ -583,18 +597,19 @@ template <int PER> struct PrepLaunch {
   static void go(dim3 grid, hipStream_t stream, const void* logits, int ldtype, int64_t T, int E, int top_k,
                  int renorm, float* tw, int32_t* ids, int bm, int64_t P, int32_t* sorted_ids, int32_t* expert_ids,
                  int32_t* ntp, int32_t* inv_pos, const uint16_t* x, int xdtype, int64_t K, int64_t ldx, uint8_t* xq,
-                 int64_t ldq, float* xs) {
+                 int64_t ldq, float* xs, int slots) {
     hipLaunchKernelGGL((moe_prep_kernel<PER, CPT>), grid, dim3(kPrepThreads), 0, stream, logits, ldtype, T, E, top_k,
-                       renorm, tw, ids, bm, P, sorted_ids, expert_ids, ntp, inv_pos, x, xdtype, K, ldx, xq, ldq, xs);
+                       renorm, tw, ids, bm, P, sorted_ids, expert_ids, ntp, inv_pos, x, xdtype, K, ldx, xq, ldq, xs,
+                       slots);
   }
   static void run(int cpt, const void* logits, int ldtype, int64_t T, int E, int top_k, int renorm, float* tw,
                   int32_t* ids, int bm, int64_t P, int32_t* sorted_ids, int32_t* expert_ids, int32_t* ntp,
                   int32_t* inv_pos, const void* x, int xdtype, int64_t K, int64_t ldx, uint8_t* xq, int64_t ldq,
-                  float* xs, hipStream_t stream) {
+                  float* xs, int slots, hipStream_t stream) {
     const dim3 grid((unsigned)(1 + (x ? T : 0)));
     const uint16_t* xp = reinterpret_cast<const uint16_t*>(x);
 #define W4A8_PREP(C) go<C>(grid, stream, logits, ldtype, T, E, top_k, renorm, tw, ids, bm, P, sorted_ids, expert_ids, \
-                           ntp, inv_pos, xp, xdtype, K, ldx, xq, ldq, xs)
+                           ntp, inv_pos, xp, xdtype, K, ldx, xq, ldq, xs, slots)
     if (cpt == 1) W4A8_PREP(1);
     else if (cpt == 2) W4A8_PREP(2);
     else if (cpt == 4) W4A8_PREP(4);
@@ -610,12 +625,12 @@ bool moe_prep_fits(int64_t T, int top_k) { return T * top_k <= kPrepMaxSlots; }
 int launch_moe_prep(const void* logits, int ldtype, int64_t T, int E, int top_k, int renorm, float* tw,
                     int32_t* ids, int bm, int64_t P, int32_t* sorted_ids, int32_t* expert_ids, int32_t* ntp,
                     int32_t* inv_pos, const void* x, int xdtype, int64_t K, int64_t ldx, uint8_t* xq, int64_t ldq,
-                    float* xs, hipStream_t stream) {
+                    float* xs, int slots, hipStream_t stream) {
   if (T <= 0) return kOk;
   const int c = quant_row_cpt(K, kPrepThreads);
   const int cpt = c >= 1 && c <= 4 ? c : 0;
   with_per<PrepLaunch>(E, cpt, logits, ldtype, T, E, top_k, renorm, tw, ids, bm, P, sorted_ids, expert_ids, ntp,
-                       inv_pos, x, xdtype, K, ldx, xq, ldq, xs, stream);
+                       inv_pos, x, xdtype, K, ldx, xq, ldq, xs, slots, stream);
   return hipGetLastError() == hipSuccess ? kOk : kErrHip;
 }
 

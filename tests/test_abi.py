@@ -88,6 +88,11 @@ def test_host_validation_rejects_before_launch(lib):
     assert lib.w4a8_tile_bytes(32, 256) == 2 * 2 * 1024
     assert lib.w4a8_tile_bytes(32, 160) == 2 * 2 * 1024
     assert lib.w4a8_moe_padded_capacity(8, 128, 16) == 8 + 129 * 15
+    # one block per slot: no more slots than experts
+    P = lib.w4a8_moe_padded_capacity(16, 8, 16)
+    rc = lib.w4a8_moe_route_slots(None, 0, 2, 8, 8, 1, 16, P, None, None, None, None, None, None, None, 0, 0, 0, None,
+                                  0, None, None)
+    assert rc == 1 and b"slots" in lib.w4a8_last_error()
 
 
 # ------------------------------------------------------------------------ provider refusals

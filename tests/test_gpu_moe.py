@@ -56,6 +56,47 @@ def test_route_align_bit_exact(kernels, oracle, dev, T):
     assert np.array_equal(inv.cpu().numpy()[: T * TOPK], rinv)
 
 
+@pytest.mark.parametrize("T", [1, 3, 8])
+def test_route_slots_layout(kernels, oracle, dev, T):
+    """w4a8_moe_route_slots (w4a8_moe's routing for decode batches): the route and x's codes equal
+    the align path's bit for bit; slot s owns padded row s*bm of a block of its own (the other rows
+    sentinels), its block's owner is its expert, inv_pos[s] = s*bm, ntp = slots*bm; and w4a8_moe on
+    such a batch takes this path and matches the oracle's forward."""
+    lg = synth.router_logits(T, E, seed=900 + T)
+    x = synth.activations(T, H, seed=901 + T).to(dev)
+    bm, S = 16, T * TOPK
+    tw, ids, sorted_ids, expert_ids, ntp, inv, xq, xs = kernels._route_align_quant(lg.to(dev), TOPK, True, E, bm, x,
+                                                                                  slots=True)
+    rtw, rids, *_ = kernels._route_align_quant(lg.to(dev), TOPK, True, E, bm, x)
+    q, sc = kernels.act_quant(x)
+    _sync()
+    assert torch.equal(tw, rtw) and torch.equal(ids, rids) and torch.equal(xq, q) and torch.equal(xs, sc)
+    assert int(ntp.item()) == S * bm
+    want = np.full(S * bm, S, dtype=np.int32)
+    want[::bm] = np.arange(S)
+    assert np.array_equal(sorted_ids.cpu().numpy()[: S * bm], want)
+    assert np.array_equal(expert_ids.cpu().numpy()[:S], ids.cpu().numpy().reshape(-1))
+    assert np.array_equal(inv.cpu().numpy()[:S], np.arange(S) * bm)
+    # more slots than experts: the align, bit for bit
+    lg8 = synth.router_logits(2, 8, seed=3).to(dev)
+    few = kernels._route_align_quant(lg8, 8, True, 8, bm, None, slots=True)
+    ref = kernels._route_align_quant(lg8, 8, True, 8, bm, None)
+    _sync()
+    for a_, b_ in zip(few[:6], ref[:6]):
+        assert torch.equal(a_, b_)
+    # w4a8_moe routes a decode batch this way
+    eng = pkg("_hip_engage")
+    w13, s13, _ = synth.int4_weight(2 * I, H, G, seed=905, asym=False, E=E, scale_floor=1e-3)
+    w2, s2, _ = synth.int4_weight(H, I, G, seed=906, asym=False, E=E, scale_floor=1e-3)
+    before = eng.counts()
+    res = kernels._moe_forward(x, w13.to(dev), s13.to(dev), None, w2.to(dev), s2.to(dev), None, lg.to(dev), TOPK,
+                               True)
+    _sync()
+    assert eng.counts_delta(before).get("w4a8_mi355x.moe_route_slots") == 1
+    rel1, rel2, y2ref = _stagewise(kernels, oracle, res, x.cpu(), w13, s13, None, w2, s2, None, list(range(T)))
+    assert rel1 <= 2e-3 and rel2 <= 2e-3
+
+
 @pytest.mark.parametrize("T", [1, 3, 16, 32, 33])
 def test_route_align_quant_bit_exact(kernels, oracle, dev, T):
     """w4a8_moe_route_align with x: route and align equal the oracle's, and x's codes and scales
