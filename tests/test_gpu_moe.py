@@ -97,15 +97,15 @@ def test_route_slots_layout(kernels, oracle, dev, T):
     assert rel1 <= 2e-3 and rel2 <= 2e-3
 
 
-@pytest.mark.parametrize("T", [1, 3, 16, 32, 33])
-def test_route_align_quant_bit_exact(kernels, oracle, dev, T):
+@pytest.mark.parametrize("T,bm", [(1, 16), (3, 16), (16, 16), (32, 16), (33, 16), (1, 64), (8, 128), (20, 64)])
+def test_route_align_quant_bit_exact(kernels, oracle, dev, T, bm):
     """w4a8_moe_route_align with x: route and align equal the oracle's, and x's codes and scales
     equal the act-quant kernel's, bit for bit. T*top_k <= 256 runs as one launch (one workgroup
-    routes and aligns, the others quantize rows); T = 33 (264 slots) takes the three-launch path."""
+    routes and aligns, the others quantize rows; up to 64 slots one wave aligns and the workgroup
+    fills); T = 33 (264 slots) takes the three-launch path."""
     lg = synth.router_logits(T, E, seed=500 + T)
     x = synth.activations(T, H, seed=T).to(dev)
     x[0] = 0  # a zero row takes the 1e-8 scale floor
-    bm = 16
     tw, ids, sorted_ids, expert_ids, ntp, inv, xq, xs = kernels._route_align_quant(lg.to(dev), TOPK, True, E, bm, x)
     q, s = kernels.act_quant(x)
     _sync()
