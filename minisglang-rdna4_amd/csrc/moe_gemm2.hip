@@ -67,7 +67,20 @@ __global__ void __launch_bounds__(kG2cMaxSlots * 64) moe_gemm2_combine_kernel(co
   float yv = 0.f;
 
   if (valid) {
-    // ---- weight tiles, scales and zero words of every K tile, issued first
+    // ---- the slot's gemm1 row: per-row fp8 quant into this wave's LDS row (act_quant.h's
+    // arithmetic: s = max(amax / 448, 1e-8), codes = e4m3(x * (1 / s)), the max being exact). The
+    // row's loads go out before the weight loads, so its quant does not wait behind them (T=1..8:
+    // 1-2% per call)
+    constexpr int kAch = (KTMAX * kTileK / 8 + 63) / 64;  // 16-byte loads per lane
+    const uint16_t* src = p.a + (int64_t)pos * p.lda;
+    const int nch = K / 8;
+    uint4 xa[kAch];
+#pragma unroll
+    for (int i = 0; i < kAch; ++i) {
+      const int c = lane + 64 * i;
+      xa[i] = c < nch ? *reinterpret_cast<const uint4*>(src + c * 8) : make_uint4(0u, 0u, 0u, 0u);
+    }
+    // ---- weight tiles, scales and zero words of every K tile, all in flight before the quant
     const uint4* wt = p.wt + (size_t)((int64_t)e * p.w_expert_tiles) * 64;
     const int kEsz = MODE == kModeI4 ? 2 : 1;
     const void* scales = reinterpret_cast<const char*>(p.scales) + (size_t)((int64_t)e * p.s_expert_stride) * kEsz;
@@ -100,17 +113,6 @@ __global__ void __launch_bounds__(kG2cMaxSlots * 64) moe_gemm2_combine_kernel(co
       }
     }
 
-    // ---- the slot's gemm1 row: per-row fp8 quant into this wave's LDS row (act_quant.h's
-    // arithmetic: s = max(amax / 448, 1e-8), codes = e4m3(x * (1 / s)), the max being exact)
-    constexpr int kAch = (KTMAX * kTileK / 8 + 63) / 64;  // 16-byte loads per lane
-    const uint16_t* src = p.a + (int64_t)pos * p.lda;
-    const int nch = K / 8;
-    uint4 xa[kAch];
-#pragma unroll
-    for (int i = 0; i < kAch; ++i) {
-      const int c = lane + 64 * i;
-      xa[i] = c < nch ? *reinterpret_cast<const uint4*>(src + c * 8) : make_uint4(0u, 0u, 0u, 0u);
-    }
     float am = 0.f;
 #pragma unroll
     for (int i = 0; i < kAch; ++i) am = fmaxf(am, amax8(xa[i], p.adtype));
