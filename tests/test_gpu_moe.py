@@ -290,9 +290,10 @@ def test_moe_asym_and_precomputed_route(kernels, oracle, dev):
     _assert_end_to_end(out, ref, y2ref, rel2, "asym + precomputed route")
 
 
-@pytest.mark.parametrize("T,bm", [(8, 16), (64, 64), (512, 128)])
+@pytest.mark.parametrize("T,bm", [(2, 16), (8, 16), (64, 64), (512, 128)])
 def test_moe_mxfp4(kernels, oracle, dev, T, bm):
-    """MXFP4 experts (e2m1 + E8M0 block-32) through the same grouped kernels, forced block_m."""
+    """MXFP4 experts (e2m1 + E8M0 block-32) through the same grouped kernels, forced block_m (T=2:
+    16 slots over 32 experts take the one-block-per-slot route)."""
     e, h, i = 32, 1024, 512
     w13, s13 = synth.mxfp4_weight(2 * i, h, seed=441, E=e)
     w2, s2 = synth.mxfp4_weight(h, i, seed=442, E=e)
