@@ -414,13 +414,23 @@ int launch_prefill_dma(const GemmArgs& p, int64_t rows_to_cover, int bm_rows, hi
   // unpacked fp8 weights plus the partials of its per-group scaling and stays at 64 x 64.
   if (bm_rows == 64) return launch_dma_modes<2, 4, 2, 2>(p, mode, (rows_to_cover + 63) / 64, stream);
   if (bm_rows == 128) return launch_dma_modes<2, 4, 4, 4>(p, mode, (rows_to_cover + 127) / 128, stream);
-  // A grid of at most half a workgroup per CU (the configs[2] M=512 calls on 4096-wide weights: 64
-  // workgroups of 256 x 128) takes 64 x 128 tiles instead, four times the workgroups: K=4096 N=4096
-  // M=512 50.7 -> 27.2 us, K=14336 N=4096 M=512 146.9 -> 80.0 us, M=1024 52.2 -> 47.2 us; grids of
-  // 192 and more measured slower that way. The tile shape does not change any output's arithmetic.
+  // Grids of at most half a workgroup per CU take smaller tiles. int4: 128 x 128 when that gives
+  // 192 or more workgroups, else 64 x 128 (the configs[2] M=512 calls, M=1024 on 4096-wide
+  // weights): K=4096 N=6144 M=512 39.5 -> 29.9 us, K=4096 N=4096 M=1024 42.4 -> 32.4 us, K=14336
+  // N=4096 M=1024 126.7 -> 94.2 us (128 x 128); K=4096 N=4096 M=512 50.7 -> 21.8 us, K=14336
+  // N=4096 M=512 146.9 -> 64.6 us (64 x 128; 128 x 128 gave 28.2 and 85.5 there). A grid of 144
+  // (K=4096 N=6144 M=768) measured slower with 128 x 128 tiles (55.5 against 48.2 us) and keeps
+  // 256 x 128. MXFP4 (256 x 256) takes 64 x 128 tiles. The tile shape does not change any
+  // output's arithmetic.
   const int64_t ncols = p.silu ? p.N / 2 : p.N;
   const int64_t bn_default = mode == kPE8M0 ? 256 : 128;
-  if ((ncols + bn_default - 1) / bn_default * ((rows_to_cover + 255) / 256) <= 128)
+  const int64_t g_default = (ncols + bn_default - 1) / bn_default * ((rows_to_cover + 255) / 256);
+  if (mode != kPE8M0 && g_default <= 128) {
+    if ((ncols + 127) / 128 * ((rows_to_cover + 127) / 128) >= 192)
+      return launch_dma_modes<4, 2, 2, 4>(p, mode, (rows_to_cover + 127) / 128, stream);
+    return launch_dma_modes<2, 4, 2, 2>(p, mode, (rows_to_cover + 63) / 64, stream);
+  }
+  if (mode == kPE8M0 && g_default <= 128)
     return launch_dma_modes<2, 4, 2, 2>(p, mode, (rows_to_cover + 63) / 64, stream);
   if (mode == kPE8M0) return launch_dma_cfg<4, 2, 4, 8, kPE8M0>(p, (rows_to_cover + 255) / 256, stream);
   return launch_dma_modes<4, 2, 4, 4>(p, mode, (rows_to_cover + 255) / 256, stream);
