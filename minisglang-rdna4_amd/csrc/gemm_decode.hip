@@ -73,20 +73,43 @@ GemvPlan plan_gemv(const GemmArgs& p, int64_t row_blocks, bool quant_src) {
   pl.amode = kAGlobal;
   if (lds_ok && quant_src && fuse_ok && qchunks <= kStageMax * threads) pl.amode = kAQuant;
   else if (lds_ok && !quant_src && schunks <= kStageMax * threads) pl.amode = kAStage;
+  // wide weights (1024+ strips): one-row fused-quant calls run 4 strips per workgroup (the silu arm
+  // 2 gate + 2 up strips), a quarter of the grid, so each CU runs about two workgroups instead of
+  // seven and quantizes the activation row twice instead of seven times: with seven, the workgroups
+  // that had their row issued weight loads that the others' row loads then queued behind (their
+  // A phase spread from 2 to 9 us); gate_up M=1 14.7 -> 13.8 us, MXFP4 K=8192 N=28672 25.8 -> 22.5
+  // us. Three strips (an uneven grid) and seven (one workgroup of 4 waves per CU) were slower. The
+  // K split is unchanged, so the output bits are too.
+  if (pl.amode == kAQuant && !p.sorted_ids && rows == 1 && strips >= 1024) pl.nstr = p.silu ? 2 : 4;
   const int64_t chunks = pl.amode == kAQuant ? qchunks : schunks;
   // staging loads per thread: exact depths for the fused quant, 4 or 8 for fp8 staging
   pl.sm = chunks <= threads ? 1 : chunks <= 2 * threads ? 2 : chunks <= 4 * threads ? 4 : 8;
   if (pl.amode == kAStage && pl.sm < 4) pl.sm = 4;
   pl.stage_bytes = pl.amode == kAGlobal ? 0 : (size_t)((lbytes + 15) / 16) * 16;
-  // the fused quant of short rows stages A before issuing any weight load: A's loads then queue
-  // behind no weight load of the CU (measured at M=1: qkv 7.8 -> 7.0 us, o_proj 6.2 -> 6.0, gate_up
-  // 15.3 -> 14.7); the 28 KiB bf16 row of K = 14336 (down) measured slower that way
-  pl.afirst = pl.amode == kAQuant && p.K <= 8192 ? 1 : 0;
+  // Window order. One-row fused-quant calls on narrow weights (K <= 8192, at most 512 strips: about
+  // a workgroup per CU) quantize A before issuing any weight load, so the row's loads meet no
+  // weight load on their way (qkv M=1 7.1 against 7.7 us with the weights issued first). Every
+  // other fused-quant call issues its first window right behind the A loads and quantizes while
+  // the weights are in flight: o_proj M=2 7.15 -> 6.95 us, down M=1 (K = 14336, with a 4-tile
+  // window) 11.2 -> 10.5 us, and the wide calls above. Staged fp8 A waits for the window before
+  // its LDS writes (equal or up to 2% faster than staging on arrival at the sweep's staged calls).
+  if (pl.amode == kAQuant)
+    pl.af = rows == 1 && p.K <= 8192 && strips <= 512 ? kWinAFirst : kWinAfterA;
+  else
+    pl.af = pl.amode == kAStage ? kWinWaitAll : kWinAfterA;
+  pl.ch = pl.amode == kAQuant && p.wfmt == kInt4 && pl.af == kWinAfterA && p.K > 8192 ? 4 : 3;
   return pl;
 }
 
 bool launch_gemv_global(const GemmArgs& p, dim3 grid, const GemvPlan& pl, hipStream_t stream) {
-  return launch_gemv_amode<kAGlobal>(p, grid, pl, stream);
+  const int ns = p.silu ? 2 * pl.nstr : pl.nstr;
+  bool ok = false;
+  if (ns == 1) ok = gemv_launch_fmt<kAGlobal, 1, kGemvChunk, kWinAfterA, true, true>(p, grid, stream, pl);
+  else if (ns == 2) ok = gemv_launch_fmt<kAGlobal, 2, kGemvChunk, kWinAfterA, true, true>(p, grid, stream, pl);
+  else if (ns == 4) ok = gemv_launch_fmt<kAGlobal, 4, kGemvChunk, kWinAfterA, true, true>(p, grid, stream, pl);
+  else return false;
+  // the sub-tile-group formats (int4 group 32/64, e2m1 with fp16 scales)
+  return ok || launch_gemv_generic(p, grid, pl, stream);
 }
 
 // row_blocks: number of 16-row blocks to launch (dense: ceil(M/16); grouped: a bound on the

@@ -160,6 +160,20 @@ constexpr int kModeI4 = 0, kModeI4Sub = 1, kModeE8M0 = 2, kModeE2M1F16 = 3, kMod
 //             arithmetic, bit for bit) into LDS.
 constexpr int kAGlobal = 0, kAStage = 1, kAQuant = 2;
 constexpr int kStageMax = 8;                // most 16-byte staging loads per thread (SM <= this)
+
+// When a wave issues its first window of weight loads (compile-time, so that the compiler's wait
+// counts stay exact; with a run-time choice it had to merge both orders and waited for every load,
+// the weights included, before it touched the A data).
+//   kWinAfterA: right after the A loads. The A data is waited for with a counted vmcnt, so the quant
+//               or staging runs while the weights are in flight.
+//   kWinAFirst: after A is quantized into LDS (fused quant): the activation row's loads meet no
+//               weight load of the workgroup on their way (one-row calls on narrow weights).
+//   kWinWaitAll: right after the A loads, and the fp8 staging waits for every load of the window
+//               before it writes LDS (staged fp8 A; measured equal or up to 2% faster than
+//               kWinAfterA on the decode sweep's staged calls).
+constexpr int kWinAfterA = 0, kWinAFirst = 1, kWinWaitAll = 2;
+// s_waitcnt vmcnt(0) in the gfx9 encoding (expcnt and lgkmcnt at their maxima: not waited for)
+constexpr int kWaitVmcnt0 = 0x0F70;
 constexpr int kStageLdsMax = 32 * 1024;     // LDS bytes of a staged A block
 
 // LDS row stride of a staged A block: K padded to whole tiles (zeros) + 16 bytes of bank skew.
@@ -175,10 +189,13 @@ __host__ __device__ inline int stage_stride(int KT) { return KT * kTileK + 16; }
 //        window of weights is in flight set the kernel's peak register count, so it is sized to the
 //        block.
 //   GPT: groups per K tile for the sub-tile-group modes (1 for the others).
-template <int NSTR, int CH, int MODE, int AMODE, bool SYM, int SM, int GPT>
-__global__ void __launch_bounds__(512) gemv_kernel(const GemmArgs p, int tpw, int afirst) {
+//   AF:  when the first window of weight loads is issued (kWinAfterA / kWinAFirst / kWinWaitAll).
+template <int NSTR, int CH, int MODE, int AMODE, bool SYM, int SM, int GPT, int AF>
+__global__ void __launch_bounds__(512) gemv_kernel(const GemmArgs p, int tpw) {
   constexpr int WFMT = (MODE == kModeE8M0 || MODE == kModeE2M1F16 || MODE == kModeNV) ? kE2M1 : kInt4;
   static_assert(MODE != kModeNV || GPT == 8, "NVFP4 tiles hold 8 groups");
+  static_assert(AF != kWinAFirst || AMODE == kAQuant, "A-first applies to the fused quant");
+  static_assert(AF != kWinWaitAll || AMODE == kAStage, "wait-all applies to fp8 staging");
   constexpr bool kStaged = AMODE != kAGlobal;
   // grouped (MoE) rows only reach the global-A kernels: the staged and fused kernels are compiled
   // without the align lookups, so their prologue has no chain of dependent argument loads
@@ -315,8 +332,8 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemmArgs p, int tpw, in
   // tile index for a slot load; past the range end it repeats the last tile (a cache hit that
   // keeps the loads unconditional)
   auto clamp_kt = [&](int kt) { return kt < kt_end ? kt : (kt_end > 0 ? kt_end - 1 : 0); };
-  // fill the window: the first CH tiles' loads are in flight while A is staged (afirst: after)
-  if (!(kStaged && afirst)) {
+  // fill the window: the first CH tiles' loads are in flight while A is staged (A-first: after)
+  if constexpr (AF != kWinAFirst) {
 #pragma unroll
     for (int t = 0; t < CH; ++t) load_tile(t, clamp_kt(kt_begin + t));
   }
@@ -379,6 +396,8 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemmArgs p, int tpw, in
     if (row_ok) row_scale = row_s(lane & 15);
     __syncthreads();
   } else if (AMODE == kAStage) {
+    // every load of the window lands before the staging writes: vmcnt(0)
+    if constexpr (AF == kWinWaitAll) __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
 #pragma unroll
     for (int i = 0; i < SM; ++i) {
       const int c = (int)threadIdx.x + i * (int)blockDim.x;
@@ -389,7 +408,7 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemmArgs p, int tpw, in
     }
     __syncthreads();
   }
-  if (kStaged && afirst) {
+  if constexpr (AF == kWinAFirst) {
 #pragma unroll
     for (int t = 0; t < CH; ++t) load_tile(t, clamp_kt(kt_begin + t));
   }
@@ -540,7 +559,8 @@ struct GemvPlan {
   int amode;    // kAGlobal / kAStage / kAQuant
   int sm;       // staging loads per thread (4 or 8) for kAStage / kAQuant
   size_t stage_bytes;  // LDS bytes of the staged A block (0 for kAGlobal)
-  int afirst;          // staged A sources: stage A before issuing any weight load
+  int af;       // when the first window of weight loads is issued (kWinAfterA / kWinAFirst / kWinWaitAll)
+  int ch;       // window of the int4 fused-quant kernels (3 or 4 tiles; the other kernels roll 4)
 };
 
 // Kernel launch of one A source; defined in the unit that instantiates it. `grid` is
@@ -548,6 +568,8 @@ struct GemvPlan {
 bool launch_gemv_global(const GemmArgs& p, dim3 grid, const GemvPlan& pl, hipStream_t stream);
 bool launch_gemv_staged(const GemmArgs& p, dim3 grid, const GemvPlan& pl, hipStream_t stream);
 bool launch_gemv_fused(const GemmArgs& p, dim3 grid, const GemvPlan& pl, hipStream_t stream);
+// the fused quant on e2m1 weights (MXFP4, NVFP4): its own unit, built in parallel with the int4 one
+bool launch_gemv_fused_e2m1(const GemmArgs& p, dim3 grid, const GemvPlan& pl, hipStream_t stream);
 // sub-tile groups (int4 group 32/64, e2m1 with fp16 scales), A read per tile
 bool launch_gemv_generic(const GemmArgs& p, dim3 grid, const GemvPlan& pl, hipStream_t stream);
 // K split (waves, tiles per wave) the GEMV runs for these arguments and row blocks
@@ -561,71 +583,93 @@ inline bool gemv_nvfp4(const GemmArgs& p) {
 // Chunk length (tiles per strip held in registers at once) of the sub-tile-group kernels: 4 for
 // short K ranges, else 8 (longer ranges roll the window through the range).
 inline int gemv_chunk(int tpw) { return tpw <= 4 ? 4 : 8; }
-// The fast-path kernels roll a 4-tile window (3 for int4 with the fused-quant A source, see the
-// launch dispatch below). Measured on MI355X at the Llama-3-8B decode
-// shapes (one row): against an 8-tile window it costs fewer VGPRs (68 against 80, so seven waves
-// per SIMD and the whole gate_up grid resident at once instead of two rounds), and it queues fewer
-// weight loads ahead of each wave's A loads on the CU, so A is ready sooner; gate_up 15.5 us
-// against 18.1 us, down 10.5 against 11.0, qkv and o_proj 4-8% faster.
+// The fast-path kernels roll a 4-tile window (3 or 4 for int4 with the fused-quant A source, chosen
+// by the planner). Measured on MI355X at the Llama-3-8B decode shapes (one row): against an 8-tile
+// window it costs fewer VGPRs (68 against 80, so seven waves per SIMD and the whole gate_up grid
+// resident at once instead of two rounds), and it queues fewer weight loads ahead of each wave's A
+// loads on the CU, so A is ready sooner; gate_up 15.5 us against 18.1 us, down 10.5 against 11.0,
+// qkv and o_proj 4-8% faster. The window does not change the summation order.
 constexpr int kGemvChunk = 4;
 
+// Block size and dynamic LDS of a launch: the staged A block plus the cross-wave reduction tile.
+inline void gemv_block_lds(const GemmArgs& p, const GemvPlan& pl, dim3& block, size_t& lds) {
+  const int nstr_k = p.silu ? 2 * pl.nstr : pl.nstr;
+  lds = pl.stage_bytes + (size_t)pl.waves * nstr_k * 4 * 64 * sizeof(float);
+  block = dim3(pl.waves * 64);
+}
+
 // Launch of one kernel variant; the staging depth only exists for staged A sources.
-template <int NS, int CHK, int MD, int AM, bool SY>
-void gemv_launch_sm(const GemmArgs& p, dim3 grid, dim3 block, size_t lds, hipStream_t stream, const GemvPlan& pl) {
+template <int NS, int CHK, int MD, int AM, bool SY, int AF>
+void gemv_launch_sm(const GemmArgs& p, dim3 grid, hipStream_t stream, const GemvPlan& pl) {
   constexpr int G = MD == kModeNV ? 8 : 1;
+  dim3 block;
+  size_t lds;
+  gemv_block_lds(p, pl, block, lds);
   if constexpr (AM == kAGlobal) {
-    hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 4, G>), grid, block, lds, stream, p, pl.tpw, pl.afirst);
+    hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 4, G, AF>), grid, block, lds, stream, p, pl.tpw);
   } else if constexpr (AM == kAStage) {
     if (pl.sm <= 4)
-      hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 4, G>), grid, block, lds, stream, p, pl.tpw, pl.afirst);
+      hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 4, G, AF>), grid, block, lds, stream, p, pl.tpw);
     else
-      hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 8, G>), grid, block, lds, stream, p, pl.tpw, pl.afirst);
+      hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 8, G, AF>), grid, block, lds, stream, p, pl.tpw);
   } else {
     if (pl.sm == 1)
-      hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 1, G>), grid, block, lds, stream, p, pl.tpw, pl.afirst);
+      hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 1, G, AF>), grid, block, lds, stream, p, pl.tpw);
     else if (pl.sm == 2)
-      hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 2, G>), grid, block, lds, stream, p, pl.tpw, pl.afirst);
+      hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 2, G, AF>), grid, block, lds, stream, p, pl.tpw);
     else if (pl.sm == 4)
-      hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 4, G>), grid, block, lds, stream, p, pl.tpw, pl.afirst);
+      hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 4, G, AF>), grid, block, lds, stream, p, pl.tpw);
     else
-      hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 8, G>), grid, block, lds, stream, p, pl.tpw, pl.afirst);
+      hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, AM, SY, 8, G, AF>), grid, block, lds, stream, p, pl.tpw);
   }
 }
 
-// Dispatch of one A source over (strips per wave, chunk) and the weight/scale formats.
-template <int AMODE>
-bool launch_gemv_amode(const GemmArgs& p, dim3 grid, const GemvPlan& pl, hipStream_t stream) {
-  const int nstr_k = p.silu ? 2 * pl.nstr : pl.nstr;
-  const size_t lds = pl.stage_bytes + (size_t)pl.waves * nstr_k * 4 * 64 * sizeof(float);
-  const dim3 block(pl.waves * 64);
-  const bool i4 = p.wfmt == kInt4 && p.group % kTileK == 0;
-  const bool e8 = p.wfmt == kE2M1 && p.sfmt == kScaleE8M0;
-  const bool nv = gemv_nvfp4(p);
-  if (!i4 && !e8 && !nv) return AMODE == kAGlobal ? launch_gemv_generic(p, grid, pl, stream) : false;
-  // int4 with the fused-quant source keeps 3 tiles per wave in flight: its weight loads queue ahead
-  // of the activation row every workgroup reads before its first MFMA, and a smaller first burst
-  // gets that row in sooner (gate_up M=1: 15.2 -> 14.8 us). The e2m1 formats, with twice the bytes
-  // per row, measured slower with 3 (MXFP4 M=1: 23.8 -> 25.1 us) and keep 4. The window does not
-  // change the summation order.
-  constexpr int kChI4 = AMODE == kAQuant ? 3 : kGemvChunk;
-#define W4A8_GEMV_LAUNCH(NS, CHK)                                                                            \
-  do {                                                                                                       \
-    if (i4 && p.zeros == nullptr)                                                                            \
-      gemv_launch_sm<NS, kChI4, kModeI4, AMODE, true>(p, grid, block, lds, stream, pl);                      \
-    else if (i4)                                                                                             \
-      gemv_launch_sm<NS, kChI4, kModeI4, AMODE, false>(p, grid, block, lds, stream, pl);                     \
-    else if (nv)                                                                                             \
-      gemv_launch_sm<NS, CHK, kModeNV, AMODE, false>(p, grid, block, lds, stream, pl);                       \
-    else                                                                                                     \
-      gemv_launch_sm<NS, CHK, kModeE8M0, AMODE, false>(p, grid, block, lds, stream, pl);                     \
-    return true;                                                                                             \
-  } while (0)
-  if (nstr_k == 1) W4A8_GEMV_LAUNCH(1, kGemvChunk);
-  if (nstr_k == 2) W4A8_GEMV_LAUNCH(2, kGemvChunk);
-  if constexpr (AMODE == kAGlobal) {
-    if (nstr_k == 4) W4A8_GEMV_LAUNCH(4, kGemvChunk);
+// Format dispatch of one (A source, strips, int4 window, window order) choice. I4 / E2: which
+// weight formats the calling unit instantiates (int4 with 128-multiple groups; MXFP4 and NVFP4).
+template <int AMODE, int NS, int CHI4, int AF, bool I4, bool E2>
+bool gemv_launch_fmt(const GemmArgs& p, dim3 grid, hipStream_t stream, const GemvPlan& pl) {
+  if constexpr (I4) {
+    if (p.wfmt == kInt4 && p.group % kTileK == 0) {
+      if (p.zeros == nullptr) gemv_launch_sm<NS, CHI4, kModeI4, AMODE, true, AF>(p, grid, stream, pl);
+      else gemv_launch_sm<NS, CHI4, kModeI4, AMODE, false, AF>(p, grid, stream, pl);
+      return true;
+    }
   }
-#undef W4A8_GEMV_LAUNCH
+  if constexpr (E2) {
+    if (gemv_nvfp4(p)) {
+      gemv_launch_sm<NS, kGemvChunk, kModeNV, AMODE, false, AF>(p, grid, stream, pl);
+      return true;
+    }
+    if (p.wfmt == kE2M1 && p.sfmt == kScaleE8M0) {
+      gemv_launch_sm<NS, kGemvChunk, kModeE8M0, AMODE, false, AF>(p, grid, stream, pl);
+      return true;
+    }
+  }
+  return false;
+}
+
+// The fused-quant kernels: strips per workgroup (1, 2, 4), int4 window (3, 4) and window order
+// (A-first or after A) as the planner chose them.
+template <bool I4, bool E2>
+bool gemv_launch_quant(const GemmArgs& p, dim3 grid, hipStream_t stream, const GemvPlan& pl) {
+  const int ns = p.silu ? 2 * pl.nstr : pl.nstr;
+  const bool first = pl.af == kWinAFirst, ch4 = pl.ch == 4;
+#define W4A8_GEMV_Q(NS, CH, AF) return gemv_launch_fmt<kAQuant, NS, CH, AF, I4, E2>(p, grid, stream, pl)
+  if (ns == 1) {
+    if (first) W4A8_GEMV_Q(1, 3, kWinAFirst);
+    if (ch4) W4A8_GEMV_Q(1, 4, kWinAfterA);
+    W4A8_GEMV_Q(1, 3, kWinAfterA);
+  }
+  if (ns == 2) {
+    if (first) W4A8_GEMV_Q(2, 3, kWinAFirst);
+    if (ch4) W4A8_GEMV_Q(2, 4, kWinAfterA);
+    W4A8_GEMV_Q(2, 3, kWinAfterA);
+  }
+  if (ns == 4 && !first) {
+    if (ch4) W4A8_GEMV_Q(4, 4, kWinAfterA);
+    W4A8_GEMV_Q(4, 3, kWinAfterA);
+  }
+#undef W4A8_GEMV_Q
   return false;
 }
 

@@ -10,16 +10,16 @@ static void launch_gpt(const GemmArgs& p, dim3 grid, dim3 block, size_t lds, int
   const int gpt = p.group >= kTileK ? 1 : kTileK / p.group;
   if constexpr (MD == kModeE2M1F16) {
     if (gpt == 8) {
-      hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, kAGlobal, SY, 4, 8>), grid, block, lds, stream, p, tpw, 0);
+      hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, kAGlobal, SY, 4, 8, kWinAfterA>), grid, block, lds, stream, p, tpw);
       return;
     }
   }
   if (gpt == 4)
-    hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, kAGlobal, SY, 4, 4>), grid, block, lds, stream, p, tpw, 0);
+    hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, kAGlobal, SY, 4, 4, kWinAfterA>), grid, block, lds, stream, p, tpw);
   else if (gpt == 2)
-    hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, kAGlobal, SY, 4, 2>), grid, block, lds, stream, p, tpw, 0);
+    hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, kAGlobal, SY, 4, 2, kWinAfterA>), grid, block, lds, stream, p, tpw);
   else if constexpr (MD == kModeE2M1F16)
-    hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, kAGlobal, SY, 4, 1>), grid, block, lds, stream, p, tpw, 0);
+    hipLaunchKernelGGL((gemv_kernel<NS, CHK, MD, kAGlobal, SY, 4, 1, kWinAfterA>), grid, block, lds, stream, p, tpw);
 }
 
 template <int NS, int CHK>
