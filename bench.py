@@ -128,7 +128,7 @@ def roofline_leg(kernels, dev, reps: int = 60) -> dict:
         traffic = json.loads(tf.read_text()).get("traffic_bytes_per_launch")
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-            "kernel": "gemv_kernel<1,3,kModeI4,kAQuant,SYM,2,1> (decode GEMV, int4 sym g128, fused act quant) "
+            "kernel": "gemv_kernel<4,3,kModeI4,kAQuant,SYM,2,1,kWinAfterA> (decode GEMV, int4 sym g128, fused act quant, 4 strips per workgroup) "
                       "K=4096 N=28672 M=1",
             "algorithmic_bytes_per_launch": nbytes, "mean_launch_us": round(mean_us, 3), "launches": reps}
 
