@@ -173,11 +173,13 @@ int w4a8_moe_gemm(const uint8_t* a_fp8, int64_t lda, const float* a_scales, int 
                   const int32_t* zeros, int wfmt, int64_t group_size, void* out, int out_dtype, int64_t ldo, int silu,
                   void* workspace, int64_t workspace_bytes, int kernel, void* stream);
 
-/* Top-k weighted combine: out[t] = sum_j topk_w[t, j] * y[inv_pos[t*top_k + j]] in f32 (H and ldy
- * multiples of 4; y 16-byte aligned, out 8-byte (16-byte for f32) aligned).
+/* Top-k weighted combine: out[t] = sum_j topk_w[t, j] * y[inv_pos[t*top_k + j]] in f32 over the slots
+ * in order, cast to out_dtype. y rows are f32, or bf16/fp16 (y_dtype), as the reference's unfused gemm2
+ * hands them over ((P, K) in the activation dtype, tools/vhip_patches/moe_experts.py:874-880). H and
+ * ldy multiples of 4; y 16-byte (f32) or 8-byte aligned, out 8-byte (16-byte for f32) aligned.
  * Replaces fp8_wmma.mmq_fp8_moe_gather_reduce (python/minisgl/quant/kernels.py:876-882). */
-int w4a8_moe_combine(const float* y, int64_t ldy, const int32_t* inv_pos, const float* topk_w, int64_t T, int top_k,
-                     int64_t H, void* out, int out_dtype, void* stream);
+int w4a8_moe_combine(const void* y, int y_dtype, int64_t ldy, const int32_t* inv_pos, const float* topk_w, int64_t T,
+                     int top_k, int64_t H, void* out, int out_dtype, void* stream);
 
 /* Fused gemm2 + top-k weighted combine of the MoE FFN for decode-sized batches: replaces
  * fp8_wmma.mmq_fp8_moe_gemm2_gather_reduce (python/minisgl/quant/kernels.py:831-850), one launch for
@@ -186,7 +188,8 @@ int w4a8_moe_combine(const float* y, int64_t ldy, const int32_t* inv_pos, const 
  * token t reads row inv_pos[s] (inv_pos < 0: dropped slot) with expert topk_ids[s], quantized per
  * row as w4a8_act_quant does, bit for bit. out (T, N) = sum_j topk_w[t, j] * gemm2(row of slot
  * (t, j)) in f32 over the slots in order, cast to out_dtype: the same bits as w4a8_act_quant +
- * w4a8_moe_gemm (decode arm, block_m) + w4a8_moe_combine. Deterministic; no workspace, no atomics.
+ * w4a8_moe_gemm (decode arm, block_m, f32 out) + w4a8_moe_combine (f32 y). Deterministic; no
+ * workspace, no atomics.
  * Formats: int4 with groups of 128+, MXFP4 (E8M0) and NVFP4; K % 128 == 0, K <= 2048, top_k <= 16
  * (w4a8_moe_gemm2_combine_supported), else kErrUnsupported (2). */
 int w4a8_moe_gemm2_combine_supported(int64_t K, int scale_fmt, int has_zeros, int wfmt, int64_t group_size, int top_k);

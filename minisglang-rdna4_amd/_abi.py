@@ -51,7 +51,7 @@ SIGNATURES = {
     "w4a8_moe_gemm": (_c_int, [_vp, _c_i64, _vp, _c_int, _vp, _vp, _vp, _c_i64, _c_int, _c_int, _c_i64,
                                _vp, _c_i64, _c_i64, _c_i64, _vp, _c_int, _vp, _c_int, _c_i64,
                                _vp, _c_int, _c_i64, _c_int, _vp, _c_i64, _c_int, _vp]),
-    "w4a8_moe_combine": (_c_int, [_vp, _c_i64, _vp, _vp, _c_i64, _c_int, _c_i64, _vp, _c_int, _vp]),
+    "w4a8_moe_combine": (_c_int, [_vp, _c_int, _c_i64, _vp, _vp, _c_i64, _c_int, _c_i64, _vp, _c_int, _vp]),
     "w4a8_moe_gemm2_combine_supported": (_c_int, [_c_i64, _c_int, _c_int, _c_int, _c_i64, _c_int]),
     "w4a8_moe_gemm2_combine": (_c_int, [_vp, _c_int, _c_i64, _vp, _vp, _vp, _c_i64, _c_int, _c_int, _c_i64, _vp,
                                         _c_i64, _c_i64, _c_i64, _vp, _c_int, _vp, _c_int, _c_i64, _vp, _c_int,

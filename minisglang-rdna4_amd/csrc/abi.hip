@@ -25,7 +25,7 @@ int launch_moe_route(const void* logits, int dtype, int64_t T, int E, int top_k,
                      int32_t* ids, hipStream_t stream);
 int launch_moe_align(const int32_t* ids, int64_t numel, int E, int bm, int64_t P, int32_t* sorted_ids,
                      int32_t* expert_ids, int32_t* ntp, int32_t* inv_pos, hipStream_t stream);
-int launch_moe_combine(const float* y, int64_t ldy, const int32_t* inv_pos, const float* tw, int64_t T,
+int launch_moe_combine(const void* y, int ydt, int64_t ldy, const int32_t* inv_pos, const float* tw, int64_t T,
                        int top_k, int64_t H, void* out, int dtype, hipStream_t stream);
 bool moe_prep_fits(int64_t T, int top_k);
 int launch_rms_norm(const void* x, int64_t ldx, void* res, int64_t ldr, const void* weight, int plus_one, float eps,
@@ -107,7 +107,7 @@ static int check_weights(const char* who, int64_t N, int64_t K, int scale_fmt, c
 
 extern "C" {
 
-int w4a8_abi_version(void) { return 1; }
+int w4a8_abi_version(void) { return 2; }
 
 const char* w4a8_last_error(void) { return g_err; }
 
@@ -525,14 +525,18 @@ int w4a8_moe_gemm2_combine(const void* a, int a_dtype, int64_t lda, const int32_
                                              topk_ids, topk_w, T, (int)E, (hipStream_t)stream), who);
 }
 
-int w4a8_moe_combine(const float* y, int64_t ldy, const int32_t* inv_pos, const float* topk_w, int64_t T, int top_k,
-                     int64_t H, void* out, int out_dtype, void* stream) {
+int w4a8_moe_combine(const void* y, int y_dtype, int64_t ldy, const int32_t* inv_pos, const float* topk_w, int64_t T,
+                     int top_k, int64_t H, void* out, int out_dtype, void* stream) {
   if (out_dtype != kBF16 && out_dtype != kF16 && out_dtype != kF32) return fail(kErrInvalid, "moe_combine: unknown dtype");
+  if (y_dtype != kBF16 && y_dtype != kF16 && y_dtype != kF32) return fail(kErrInvalid, "moe_combine: unknown y dtype");
   if (ldy < H) return fail(kErrInvalid, "moe_combine: ldy < H");
-  if (H % 4 || ldy % 4 || !aligned16(y) || (reinterpret_cast<uintptr_t>(out) & (out_dtype == kF32 ? 15u : 7u)))
-    return fail(kErrInvalid, "moe_combine: H and ldy must be multiples of 4 with y 16-byte and out %d-byte aligned",
-                out_dtype == kF32 ? 16 : 8);
-  return hip_status(launch_moe_combine(y, ldy, inv_pos, topk_w, T, top_k, H, out, out_dtype, (hipStream_t)stream),
+  const uintptr_t ymask = y_dtype == kF32 ? 15u : 7u;
+  if (H % 4 || ldy % 4 || (reinterpret_cast<uintptr_t>(y) & ymask) ||
+      (reinterpret_cast<uintptr_t>(out) & (out_dtype == kF32 ? 15u : 7u)))
+    return fail(kErrInvalid, "moe_combine: H and ldy must be multiples of 4 with y %d-byte and out %d-byte aligned",
+                y_dtype == kF32 ? 16 : 8, out_dtype == kF32 ? 16 : 8);
+  return hip_status(launch_moe_combine(y, y_dtype, ldy, inv_pos, topk_w, T, top_k, H, out, out_dtype,
+                                       (hipStream_t)stream),
                     "moe_combine");
 }
 

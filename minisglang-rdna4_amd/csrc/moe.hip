@@ -516,9 +516,11 @@ moe_prep_kernel(const void* __restrict__ logits, int ldtype, int64_t T, int E, i
   align_block<kPrepThreads, 64 * PER, 0>(ids_s, T * top_k, E, bm, P, sorted_ids, expert_ids, ntp, inv_pos);
 }
 
-// Four channels per thread: 16-byte loads of y, one 8-byte (or 16-byte f32) store.
+// Four channels per thread: 16-byte (f32 y) or 8-byte (bf16/fp16 y) loads of y, one 8-byte (or
+// 16-byte f32) store. YF32: y holds f32 rows; else rows in ydt (bf16/fp16), widened exactly.
+template <bool YF32>
 __global__ void __launch_bounds__(256)
-moe_combine_kernel(const float* __restrict__ y, int64_t ldy, const int32_t* __restrict__ inv_pos,
+moe_combine_kernel(const void* __restrict__ yv, int ydt, int64_t ldy, const int32_t* __restrict__ inv_pos,
                    const float* __restrict__ tw, int64_t T, int top_k, int64_t H, void* __restrict__ out, int dtype) {
   const int64_t h = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
   if (h >= H) return;
@@ -528,7 +530,14 @@ moe_combine_kernel(const float* __restrict__ y, int64_t ldy, const int32_t* __re
       const int64_t pos = inv_pos[t * top_k + j];
       if (pos >= 0) {
         const float w = tw[t * top_k + j];
-        const float4 v = *reinterpret_cast<const float4*>(y + pos * ldy + h);
+        float4 v;
+        if constexpr (YF32) {
+          v = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(yv) + pos * ldy + h);
+        } else {
+          const uint2 r = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(yv) + pos * ldy + h);
+          v = make_float4(from_dtype((uint16_t)(r.x & 0xffffu), ydt), from_dtype((uint16_t)(r.x >> 16), ydt),
+                          from_dtype((uint16_t)(r.y & 0xffffu), ydt), from_dtype((uint16_t)(r.y >> 16), ydt));
+        }
         // one FMA per slot, in slot order (the fused gemm2 + combine does the same)
         acc.x = fmaf(w, v.x, acc.x);
         acc.y = fmaf(w, v.y, acc.y);
@@ -634,11 +643,16 @@ int launch_moe_prep(const void* logits, int ldtype, int64_t T, int E, int top_k,
   return hipGetLastError() == hipSuccess ? kOk : kErrHip;
 }
 
-int launch_moe_combine(const float* y, int64_t ldy, const int32_t* inv_pos, const float* tw, int64_t T,
+int launch_moe_combine(const void* y, int ydt, int64_t ldy, const int32_t* inv_pos, const float* tw, int64_t T,
                        int top_k, int64_t H, void* out, int dtype, hipStream_t stream) {
   if (T <= 0) return kOk;
   dim3 grid((unsigned)((H / 4 + 255) / 256), (unsigned)(T < 65535 ? T : 65535));
-  hipLaunchKernelGGL(moe_combine_kernel, grid, dim3(256), 0, stream, y, ldy, inv_pos, tw, T, top_k, H, out, dtype);
+  if (ydt == kF32)
+    hipLaunchKernelGGL(moe_combine_kernel<true>, grid, dim3(256), 0, stream, y, ydt, ldy, inv_pos, tw, T, top_k, H,
+                       out, dtype);
+  else
+    hipLaunchKernelGGL(moe_combine_kernel<false>, grid, dim3(256), 0, stream, y, ydt, ldy, inv_pos, tw, T, top_k, H,
+                       out, dtype);
   return hipGetLastError() == hipSuccess ? kOk : kErrHip;
 }
 

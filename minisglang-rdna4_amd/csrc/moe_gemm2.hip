@@ -16,7 +16,9 @@
 // Bits: a slot's row sum follows the grouped gemm2's K split (K tiles in runs of tpw, one
 // accumulator per run started from zero, the runs summed in order) with the same per-tile MFMA
 // and FMA sequence, and the combine is the unfused combine's FMA chain, so the output equals the
-// unfused path (act quant, w4a8_moe_gemm decode arm, w4a8_moe_combine) bit for bit.
+// unfused path run with an f32 intermediate (act quant, w4a8_moe_gemm decode arm into f32,
+// w4a8_moe_combine) bit for bit. Like the reference's fused gemm2 + gather-reduce, the slot rows
+// are summed unrounded; its unfused gemm2 hands them over in the activation dtype.
 #include "gemv.h"
 
 namespace w4a8 {

@@ -683,9 +683,12 @@ _MOE_SLOTS_MAX = int(os.environ.get("W4A8_MOE_SLOTS_MAX", "8"))
 
 def _moe_forward(x, w13, w13_scales, w13_zeros, w2, w2_scales, w2_zeros, gating_output, top_k, renormalize, *,
                  topk_weights=None, topk_ids=None, block_m=None, weight_is_e2m1=False, activation="silu",
-                 x_fp8=None, act_scales=None) -> dict:
+                 x_fp8=None, act_scales=None, y2_dtype=None) -> dict:
     """w4a8_moe's pipeline; returns the output and every intermediate (route, align, the (P, inter)
-    gemm1 buffer) so each stage can be checked on its own."""
+    gemm1 buffer) so each stage can be checked on its own. y2_dtype: dtype of the unfused gemm2's
+    (P, K) rows handed to the combine: x's dtype by default, as the reference's unfused gemm2 returns
+    them (tools/vhip_patches/moe_experts.py:874-880, python/minisgl/quant/kernels.py:866-882);
+    torch.float32 keeps them unrounded, which is what the fused gemm2 + combine sums."""
     M, K = x.shape
     E = w13.shape[0]
     _grp = (K // w13_scales.shape[1]) if w13_scales.dim() == 3 else -1
@@ -784,14 +787,18 @@ def _moe_forward(x, w13, w13_scales, w13_zeros, w2, w2_scales, w2_zeros, gating_
     rows = min(P, (numel // block_m + min(E, numel)) * block_m)
     _abi.check(lib.w4a8_act_quant(_abi.ptr(buf2), _abi.dtype_code(x.dtype), rows, inter, inter, _abi.ptr(q2), inter,
                                   _abi.ptr(s2), _abi.ptr(ntp), _abi.stream_of(x)), "w4a8_moe act_quant(gemm2)")
-    y2 = torch.empty((P, K), dtype=torch.float32, device=x.device)
+    # gemm2's (P, K) rows in x's dtype, as the reference's unfused gemm2 returns them; the combine
+    # sums them in f32
+    ydt = x.dtype if y2_dtype is None else y2_dtype
+    y2 = torch.empty((P, K), dtype=ydt, device=x.device)
     engaged(f"w4a8_mi355x.moe_gemm2({arm_name}{e2})")
     _moe_gemm(q2, inter, s2, 0, sorted_ids, expert_ids, ntp, numel, top_k, block_m, P, t2, E, K, inter,
-              w2s, s2f, w2z, wfmt, _grp2, y2, _abi.F32, K, False, arm, "w4a8_moe gemm2")
+              w2s, s2f, w2z, wfmt, _grp2, y2, _abi.dtype_code(ydt), K, False, arm, "w4a8_moe gemm2")
     out = torch.empty((M, K), dtype=x.dtype, device=x.device)
     engaged("w4a8_mi355x.moe_combine")
-    _abi.check(lib.w4a8_moe_combine(_abi.ptr(y2), K, _abi.ptr(inv), _abi.ptr(topk_weights), M, top_k, K,
-                                    _abi.ptr(out), _abi.dtype_code(x.dtype), _abi.stream_of(x)), "w4a8_moe combine")
+    _abi.check(lib.w4a8_moe_combine(_abi.ptr(y2), _abi.dtype_code(ydt), K, _abi.ptr(inv), _abi.ptr(topk_weights), M,
+                                    top_k, K, _abi.ptr(out), _abi.dtype_code(x.dtype), _abi.stream_of(x)),
+               "w4a8_moe combine")
     return {"out": out, "buf2": buf2, "y2": y2, "topk_weights": topk_weights, "topk_ids": topk_ids,
             "sorted_ids": sorted_ids, "expert_ids": expert_ids, "ntp": ntp, "inv_pos": inv, "block_m": block_m,
             "fused_gemm2": False}
@@ -880,7 +887,7 @@ def _w4a16_moe_forward(x, w13, w13_scales, w13_zeros, w2, w2_scales, w2_zeros, *
     tw_v = topk_weights.repeat(1, nt).contiguous()
     out = torch.empty((M, K), dtype=x.dtype, device=dev)
     engaged("w4a8_mi355x.moe_combine")
-    _abi.check(lib.w4a8_moe_combine(_abi.ptr(y2), K, _abi.ptr(inv), _abi.ptr(tw_v), M, nt * top_k, K, _abi.ptr(out),
+    _abi.check(lib.w4a8_moe_combine(_abi.ptr(y2), _abi.F32, K, _abi.ptr(inv), _abi.ptr(tw_v), M, nt * top_k, K, _abi.ptr(out),
                                     _abi.dtype_code(x.dtype), _abi.stream_of(x)), f"{what} combine")
     return {"out": out, "h": h, "topk_weights": topk_weights, "topk_ids": topk_ids, "sorted_ids": sorted_ids,
             "expert_ids": expert_ids, "ntp": ntp, "inv_pos": inv, "block_m": block_m, "terms": nt}

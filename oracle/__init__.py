@@ -55,7 +55,7 @@ def lib() -> ctypes.CDLL:
         L.w4o_moe_align.argtypes = [vp, i64, i64, i64, vp, vp, vp, vp]
         L.w4o_moe_forward.restype = None
         L.w4o_moe_forward.argtypes = [vp, ci, i64, i64, i64, i64, i64, vp, vp, vp, ctypes.c_int32, i64,
-                                      vp, vp, vp, vp, vp, vp, ci, ci, i64, i64, vp, vp]
+                                      vp, vp, vp, vp, vp, vp, ci, ci, i64, i64, vp, vp, ci]
         L.w4o_w4a16_moe_forward.restype = None
         L.w4o_w4a16_moe_forward.argtypes = [vp, ci, i64, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, ci, ci,
                                             i64, i64, vp, vp]
@@ -184,9 +184,11 @@ def moe_align(ids: np.ndarray, E: int, bm: int):
 
 
 def moe_forward(x_bits, dtype, tw, sorted_ids, expert_ids, ntp, bm, top_k, w13, s13, z13, w2, s2, z2,
-                e2m1=False, with_buf2=False, nvfp4=False):
+                e2m1=False, with_buf2=False, nvfp4=False, round_y2=False):
     """Full grouped W4A8 MoE forward in f64 -> (T, H) (before the dtype cast). nvfp4: e4m3 block-scale
-    bytes in s13/s2 and the (E, N) f32 globals in z13/z2."""
+    bytes in s13/s2 and the (E, N) f32 globals in z13/z2. round_y2: each slot's gemm2 row rounded to
+    the dtype before the combine (the reference's unfused gemm2 + gather-reduce); else unrounded (its
+    fused gemm2 + gather-reduce)."""
     x = np.ascontiguousarray(x_bits, dtype=np.uint16)
     T, H = x.shape
     E, N1 = w13.shape[0], w13.shape[1]
@@ -206,7 +208,7 @@ def moe_forward(x_bits, dtype, tw, sorted_ids, expert_ids, ntp, bm, top_k, w13, 
     twc = np.ascontiguousarray(tw, dtype=np.float32)
     lib().w4o_moe_forward(_p(x), dtype, T, H, I, E, top_k, _p(twc), _p(np.ascontiguousarray(sorted_ids, dtype=np.int32)),
                           _p(np.ascontiguousarray(expert_ids, dtype=np.int32)), ntp, bm, _p(w13c), _p(a13), _p(z13c),
-                          _p(w2c), _p(a2), _p(z2c), fmt, int(e2m1), g1, g2, _p(out), _p(buf2))
+                          _p(w2c), _p(a2), _p(z2c), fmt, int(e2m1), g1, g2, _p(out), _p(buf2), int(round_y2))
     return (out, buf2) if with_buf2 else out
 
 

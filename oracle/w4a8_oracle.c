@@ -354,7 +354,11 @@ uint16_t w4o_silu_mul(double gate, double up, int dtype) {
 /* Grouped W4A8 MoE forward: restates python/minisgl/quant/kernels.py:562-882 (route -> align -> */
 /* gemm1 + fused silu*up (output in x.dtype) -> per-row act-quant of the (P, inter) buffer ->     */
 /* gemm2 -> top-k weighted combine in f32, cast to x.dtype); the combine order and the f32        */
-/* accumulator follow mmq_fp8_moe_gather_reduce (kernels.py:876-882). Weights in op layout:       */
+/* accumulator follow mmq_fp8_moe_gather_reduce (kernels.py:876-882). round_y2 != 0: each slot's   */
+/* gemm2 row is rounded to x.dtype before the combine, as the reference's unfused gemm2 hands it   */
+/* over ((P, K) in the activation dtype: tools/vhip_patches/moe_experts.py:874-880); 0: the row   */
+/* enters the combine unrounded, as in the fused gemm2 + gather-reduce (kernels.py:831-850).     */
+/* Weights in op layout:                                                                          */
 /* w13 (E, 2I, H/8), s13 (E, H/g, 2I), z13 (E, H/g, 2I/8) or NULL; w2 (E, H, I/8), s2 (E, I/g, H).*/
 /* Uses the caller's route (tw, ids) and align (sorted_ids, expert_ids, ntp).                    */
 /* out: (T, H) f64 before the final dtype cast.                                                   */
@@ -365,7 +369,7 @@ void w4o_moe_forward(const uint16_t* x, int dtype, int64_t T, int64_t H, int64_t
                      const int32_t* w13, const void* s13, const int32_t* z13,
                      const int32_t* w2, const void* s2, const int32_t* z2,
                      int scale_fmt, int e2m1, int64_t g1, int64_t g2, double* out,
-                     uint16_t* buf2_out /* optional (ntp, I) */) {
+                     uint16_t* buf2_out /* optional (ntp, I) */, int round_y2) {
   int64_t N1 = 2 * I;
   uint8_t* xq = (uint8_t*)malloc((size_t)(T * H));
   float* xs = (float*)malloc(sizeof(float) * (size_t)T);
@@ -394,6 +398,8 @@ void w4o_moe_forward(const uint16_t* x, int dtype, int64_t T, int64_t H, int64_t
     w4o_gemm(b2q, &s2v, 1, I, w2 + e * sz2, H, (const char*)s2 + e * szs2 * sb, scale_fmt,
              z2 ? z2 + e * szz2 : NULL, e2m1, g2, y2);
     double wgt = (double)tw[r];
+    if (round_y2)
+      for (int64_t j = 0; j < H; ++j) y2[j] = (double)from_dt(to_dt((float)y2[j], dtype), dtype);
     for (int64_t j = 0; j < H; ++j) out[t * H + j] += wgt * y2[j];
   }
   free(y2); free(b2q); free(b2); free(h); free(xs); free(xq);

@@ -169,12 +169,17 @@ def test_route_ties_keep_lower_index(kernels, dev):
     assert ids.cpu().tolist() == [[7, 1, 2], [0, 1, 2], [0, 1, 2]]
 
 
-def _oracle_moe(oracle, x, lg, w13, s13, w2, s2, bm, e2m1=False, z13=None, z2=None):
+def _oracle_moe(oracle, x, lg, w13, s13, w2, s2, bm, e2m1=False, z13=None, z2=None, round_y2=False):
     tw, ids = oracle.moe_route(lg.float().numpy(), TOPK, True)
     sorted_ids, expert_ids, ntp, _ = oracle.moe_align(ids, w13.shape[0], bm)
     f = lambda t: None if t is None else t.numpy()
     return oracle.moe_forward(synth.bits16(x), 0, tw, sorted_ids, expert_ids, ntp, bm, TOPK, w13.numpy(), s13.numpy(),
-                              f(z13), w2.numpy(), s2.numpy(), f(z2), e2m1=e2m1)
+                              f(z13), w2.numpy(), s2.numpy(), f(z2), e2m1=e2m1, round_y2=round_y2)
+
+
+def _round_bf16(y):
+    """f64 values rounded to bf16 through f32 (the GPU rounds its f32 gemm2 rows once)."""
+    return torch.from_numpy(np.asarray(y, dtype=np.float32)).to(torch.bfloat16).double().numpy()
 
 
 def _subset(T, n=32):
@@ -188,7 +193,9 @@ def _stagewise(kernels, oracle, res, x, w13, s13, z13, w2, s2, z2, rows_tokens, 
     """Check gemm1+silu and (act-quant, gemm2, combine) separately against the oracle, the second
     stage fed with the GPU's own gemm1 buffer. Returns (rel gemm1, rel combine, stage-2 reference
     (tokens, H): the oracle's requant + gemm2 + combine of the GPU's gemm1 buffer). For NVFP4,
-    z13/z2 are the (E, N) f32 globals and the scales e4m3 bytes."""
+    z13/z2 are the (E, N) f32 globals and the scales e4m3 bytes. The unfused path hands the
+    combine each slot's gemm2 row in x's dtype (bf16 here), as the reference's unfused gemm2 does;
+    the fused gemm2 + combine sums them unrounded: the reference follows whichever ran."""
     top_k = res["topk_ids"].shape[1]
     sorted_ids = res["sorted_ids"].cpu().numpy()
     expert_ids = res["expert_ids"].cpu().numpy()
@@ -216,6 +223,8 @@ def _stagewise(kernels, oracle, res, x, w13, s13, z13, w2, s2, z2, rows_tokens, 
             g1_err.append(oracle.bf16_to_f32(got_b2).astype(np.float64) - g1_ref[-1])
             q2, s2v = oracle.act_quant(got_b2[None, :], 0)
             y = oracle.gemm(q2, s2v, w2[e].numpy(), s2[e].numpy(), f(z2, e), I // s2.shape[1], e2m1, nvfp4)[0]
+            if not res["fused_gemm2"]:
+                y = _round_bf16(y)
             acc += tw[t, j] * y
         y_ref.append(acc)
         y_got.append(out[t])
@@ -260,7 +269,7 @@ def test_config4_moe(kernels, oracle, dev, experts, T):
     assert rel1 <= 2e-3 and rel2 <= 2e-3
     subt = torch.tensor(sub)
     bm_sub = kernels._moe_block_m(len(sub), E, TOPK, flag_gemm1=True)
-    ref = _oracle_moe(oracle, x[subt], lg[subt], w13, s13, w2, s2, bm_sub)
+    ref = _oracle_moe(oracle, x[subt], lg[subt], w13, s13, w2, s2, bm_sub, round_y2=not res["fused_gemm2"])
     _assert_end_to_end(out[subt.to(dev)], ref, y2ref, rel2, f"config4 T={T}")
 
 
@@ -286,7 +295,7 @@ def test_moe_asym_and_precomputed_route(kernels, oracle, dev):
     assert rel1 <= 2e-3 and rel2 <= 2e-3
     sorted_ids, expert_ids, ntp, _ = oracle.moe_align(ids, e, 16)
     ref = oracle.moe_forward(synth.bits16(x), 0, tw, sorted_ids, expert_ids, ntp, 16, 4, w13.numpy(), s13.numpy(),
-                             z13.numpy(), w2.numpy(), s2.numpy(), z2.numpy())
+                             z13.numpy(), w2.numpy(), s2.numpy(), z2.numpy(), round_y2=not res["fused_gemm2"])
     _assert_end_to_end(out, ref, y2ref, rel2, "asym + precomputed route")
 
 
@@ -307,7 +316,7 @@ def test_moe_mxfp4(kernels, oracle, dev, T, bm):
     rel1, rel2, y2ref = _stagewise(kernels, oracle, res, x, w13, s13, None, w2, s2, None, subl, e2m1=True)
     assert rel1 <= 2e-3 and rel2 <= 2e-3, f"mxfp4 T={T} bm={bm}: stages {rel1:.3e} {rel2:.3e}"
     sub = torch.tensor(subl)
-    ref = _oracle_moe(oracle, x[sub], lg[sub], w13, s13, w2, s2, 16, e2m1=True)
+    ref = _oracle_moe(oracle, x[sub], lg[sub], w13, s13, w2, s2, 16, e2m1=True, round_y2=not res["fused_gemm2"])
     _assert_end_to_end(out[sub.to(dev)], ref, y2ref, rel2, f"mxfp4 T={T} bm={bm}")
 
 
@@ -350,8 +359,8 @@ def _fmt_experts(fmt, e, h, i, seed):
 def test_moe_fused_gemm2_combine_bit_exact(kernels, dev, monkeypatch, fmt, T, bm):
     """The one-launch gemm2 + top-k combine (requant of the gemm1 rows in its prologue; the
     reference's mmq_fp8_moe_gemm2_gather_reduce, python/minisgl/quant/kernels.py:831-850) gives
-    the bits of the unfused path (act quant, gemm2 into (P, H) f32, combine), and the same bits
-    run to run. The fused kernel reproduces the grouped gemm2's K split, which block_m and the grid
+    the bits of the unfused path run with an f32 intermediate (act quant, gemm2 into (P, H) f32,
+    combine), and the same bits run to run. The fused kernel reproduces the grouped gemm2's K split, which block_m and the grid
     set (block_m 32 covers a second split), and 2 of the experts are dropped from one run's route
     (ids past E, as an EP rank's non-local experts), which both paths skip."""
     e, h, i, k = 32, 1024, 768, 8
@@ -370,7 +379,7 @@ def test_moe_fused_gemm2_combine_bit_exact(kernels, dev, monkeypatch, fmt, T, bm
         monkeypatch.setattr(kernels, "_MOE_G2FUSE", True)
         fused = [kernels._moe_forward(x, *args, None, k, True, **kw) for _ in range(2)]
         monkeypatch.setattr(kernels, "_MOE_G2FUSE", False)
-        plain = kernels._moe_forward(x, *args, None, k, True, **kw)
+        plain = kernels._moe_forward(x, *args, None, k, True, y2_dtype=torch.float32, **kw)
         _sync()
         assert fused[0]["fused_gemm2"] and not plain["fused_gemm2"]
         for f in fused:
@@ -559,5 +568,5 @@ def test_moe_edge_routes(kernels, oracle, dev, E_, k, T):
     sub = torch.tensor(rows)
     sorted_ids, expert_ids, ntp, _ = oracle.moe_align(ids[rows], E_, 16)
     ref = oracle.moe_forward(synth.bits16(x[sub]), 0, tw[rows], sorted_ids, expert_ids, ntp, 16, k, w13.numpy(),
-                             s13.numpy(), None, w2.numpy(), s2.numpy(), None)
+                             s13.numpy(), None, w2.numpy(), s2.numpy(), None, round_y2=not res["fused_gemm2"])
     _assert_end_to_end(res["out"][sub.to(dev)], ref, y2ref, rel2, f"moe E={E_} k={k} T={T}")

@@ -289,7 +289,8 @@ def test_silu_mul_replica(oracle):
 
 
 def test_moe_forward_matches_composition(oracle):
-    """The fused oracle MoE == route -> align -> per-slot gemm1 -> silu -> act-quant -> gemm2 -> combine."""
+    """The fused oracle MoE == route -> align -> per-slot gemm1 -> silu -> act-quant -> gemm2 -> combine,
+    with each slot's gemm2 row entering the combine unrounded, or (round_y2) rounded to x's dtype."""
     T, H, I, E, k, g = 5, 256, 128, 8, 2, 128
     x = synth.activations(T, H, seed=31)
     w13, s13, _ = synth.int4_weight(2 * I, H, g, seed=32, asym=False, E=E)
@@ -301,6 +302,7 @@ def test_moe_forward_matches_composition(oracle):
     out = oracle.moe_forward(synth.bits16(x), 0, tw, sorted_ids, expert_ids, ntp, 16, k, w13, s13, None, w2, s2, None)
     xq, xs = oracle.act_quant(synth.bits16(x), 0)
     ref = np.zeros((T, H))
+    ref_r = np.zeros((T, H))
     for t in range(T):
         for j in range(k):
             e = ids[t, j]
@@ -309,7 +311,15 @@ def test_moe_forward_matches_composition(oracle):
             q2, s2v = oracle.act_quant(b2[None, :], 0)
             y = oracle.gemm(q2, s2v, w2[e], s2[e], None, g)[0]
             ref[t] += tw[t, j] * y
+            # the unfused contract: the slot's gemm2 row reaches the combine in x's dtype (torch's
+            # RNE f32 -> bf16 cast, independent of the oracle's own rounding helpers)
+            yr = torch.from_numpy(y.astype(np.float32)).to(torch.bfloat16).double().numpy()
+            ref_r[t] += tw[t, j] * yr
     np.testing.assert_allclose(out, ref, rtol=1e-9, atol=1e-9)
+    out_r = oracle.moe_forward(synth.bits16(x), 0, tw, sorted_ids, expert_ids, ntp, 16, k, w13, s13, None, w2, s2, None,
+                               round_y2=True)
+    np.testing.assert_allclose(out_r, ref_r, rtol=1e-9, atol=1e-9)
+    assert not np.allclose(out_r, out, rtol=1e-6, atol=0)  # the rounding is really applied
 
 
 # ------------------------------------------------------------------------------- RMSNorm producer
