@@ -97,21 +97,23 @@ __global__ void __launch_bounds__(kG2cMaxSlots * 64) moe_gemm2_combine_kernel(co
     uint32_t zw[(MODE == kModeI4 && !SYM) ? KTMAX : 1];
     int sb[MODE == kModeE8M0 ? KTMAX : 1];
     uint8_t nvs[MODE == kModeNV ? KTMAX : 1][8];
+    // every slot up to KTMAX is loaded, those past KT from tile KT-1 again (a cache hit, never
+    // used): a guard per tile made the compiler finish each tile's scale before issuing the next
+    // tile, one memory round trip per K tile
 #pragma unroll
     for (int kt = 0; kt < KTMAX; ++kt) {
-      if (kt < KT) {
-        raw[kt] = bload128_nt(rs_w, (uint32_t)lane * 16, (uint32_t)((strip * KT + kt) * kTileBytes));
-        if (MODE == kModeI4) {
-          const int g = kt >> gshift;
-          sc[kt] = bload16(rs_s, (uint32_t)n * 2, (uint32_t)(g * N * 2));
-          if (!SYM) zw[(MODE == kModeI4 && !SYM) ? kt : 0] = bload32(rs_z, (uint32_t)(n / 8) * 4, (uint32_t)(g * (N / 8) * 4));
-        } else if (MODE == kModeE8M0) {
-          sb[MODE == kModeE8M0 ? kt : 0] = (int)bload8(rs_s, (uint32_t)((lane >> 4) * N + n), (uint32_t)(kt * 4 * N));
-        } else {
+      const int kc = kt < KT ? kt : KT - 1;
+      raw[kt] = bload128_nt(rs_w, (uint32_t)lane * 16, (uint32_t)((strip * KT + kc) * kTileBytes));
+      if (MODE == kModeI4) {
+        const int g = kc >> gshift;
+        sc[kt] = bload16(rs_s, (uint32_t)n * 2, (uint32_t)(g * N * 2));
+        if (!SYM) zw[(MODE == kModeI4 && !SYM) ? kt : 0] = bload32(rs_z, (uint32_t)(n / 8) * 4, (uint32_t)(g * (N / 8) * 4));
+      } else if (MODE == kModeE8M0) {
+        sb[MODE == kModeE8M0 ? kt : 0] = (int)bload8(rs_s, (uint32_t)((lane >> 4) * N + n), (uint32_t)(kc * 4 * N));
+      } else {
 #pragma unroll
-          for (int ss = 0; ss < 8; ++ss)
-            nvs[MODE == kModeNV ? kt : 0][ss] = bload8(rs_s, (uint32_t)n, (uint32_t)((kt * 8 + ss) * N));
-        }
+        for (int ss = 0; ss < 8; ++ss)
+          nvs[MODE == kModeNV ? kt : 0][ss] = bload8(rs_s, (uint32_t)n, (uint32_t)((kc * 8 + ss) * N));
       }
     }
 
