@@ -137,6 +137,24 @@ int w4a8_moe_route_slots(const void* logits, int logits_dtype, int64_t T, int64_
                          int32_t* expert_ids, int32_t* ntp, int32_t* inv_pos, const void* x, int x_dtype, int64_t K,
                          int64_t ldx, uint8_t* x_fp8, int64_t ldq, float* x_scales, void* stream);
 
+/* Route + slots + gemm1 of a decode-sized MoE batch in one launch: the outputs of
+ * w4a8_moe_route_slots (topk_w, topk_ids, sorted_ids, expert_ids, ntp, inv_pos; slots whose token
+ * has no expert left to choose, NaN logits, get inv_pos -1 and a sentinel block) and of
+ * w4a8_moe_gemm on them (decode arm, silu, gemm1 of x: out (P, N/2) at rows s*block_m), bit for
+ * bit, without the per-token quant of x in memory. Fuses the reference's moe_hip.moe_route_align
+ * (python/minisgl/quant/kernels.py:423-447) with the gemm1 of mmq_fp8_moe_gemm1_silu
+ * (kernels.py:744-773) for the calls where w4a8_moe gives every slot a block of its own; the
+ * router runs inside every workgroup of the GEMV. x: (T, K) bf16/fp16, 16-byte aligned rows.
+ * Needs block_m < 64, T*top_k <= min(E, 64), T*top_k*block_m <= P, E <= 256 and the GEMV's fast
+ * formats (int4 with groups of 128+, MXFP4, NVFP4), else kErrUnsupported (2): the caller then runs
+ * w4a8_moe_route_slots and w4a8_moe_gemm. */
+int w4a8_moe_route_gemm1(const void* logits, int logits_dtype, int64_t T, int64_t E, int top_k, int renormalize,
+                         const void* x, int x_dtype, int64_t ldx, int block_m, int64_t P, const void* w_tile, int64_t N,
+                         int64_t K, const void* scales, int scale_fmt, const int32_t* zeros, int wfmt,
+                         int64_t group_size, float* topk_w, int32_t* topk_ids, int32_t* sorted_ids,
+                         int32_t* expert_ids, int32_t* ntp, int32_t* inv_pos, void* out, int out_dtype, int64_t ldo,
+                         void* stream);
+
 /* RMSNorm producer with the per-token fp8 quant of its output as an epilogue. Replaces tail_hip's
  * rms_norm / rms_norm_add / rms_norm_quant / rms_norm_add_quant (python/minisgl/layers/norm.py:9-58,
  * 134-168): with residual non-NULL, residual <- x + residual (in place, in the activation dtype) and

@@ -16,6 +16,8 @@ _LIB_PATH = _PKG / "_lib" / "libw4a8_mi355x.so"
 BF16, F16, F32 = 0, 1, 2
 SCALE_F16, SCALE_E8M0, SCALE_E4M3 = 0, 1, 2
 W_INT4, W_E2M1 = 0, 1
+# status codes (w4a8_mi355x.h)
+ERR_UNSUPPORTED = 2
 KERNEL_AUTO, KERNEL_DECODE, KERNEL_PREFILL = 0, 1, 2
 
 _c_i64 = ctypes.c_int64
@@ -56,6 +58,9 @@ SIGNATURES = {
     "w4a8_moe_gemm2_combine": (_c_int, [_vp, _c_int, _c_i64, _vp, _vp, _vp, _c_i64, _c_int, _c_int, _c_i64, _vp,
                                         _c_i64, _c_i64, _c_i64, _vp, _c_int, _vp, _c_int, _c_i64, _vp, _c_int,
                                         _c_i64, _vp]),
+    "w4a8_moe_route_gemm1": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _c_int, _c_int, _vp, _c_int, _c_i64, _c_int,
+                                      _c_i64, _vp, _c_i64, _c_i64, _vp, _c_int, _vp, _c_int, _c_i64, _vp, _vp, _vp,
+                                      _vp, _vp, _vp, _vp, _c_int, _c_i64, _vp]),
     "w4a16_act_split": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _c_i64, _vp, _c_i64, _vp, _vp]),
     "w4a16_linear_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_int]),
     "w4a16_linear": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _c_i64, _vp, _c_i64, _vp, _c_int, _vp, _c_int, _c_i64,

@@ -28,6 +28,7 @@ int launch_moe_align(const int32_t* ids, int64_t numel, int E, int bm, int64_t P
 int launch_moe_combine(const void* y, int ydt, int64_t ldy, const int32_t* inv_pos, const float* tw, int64_t T,
                        int top_k, int64_t H, void* out, int dtype, hipStream_t stream);
 bool moe_prep_fits(int64_t T, int top_k);
+int launch_moe_route_gemm1(const GemmArgs& p, int64_t row_blocks, hipStream_t stream);
 int launch_rms_norm(const void* x, int64_t ldx, void* res, int64_t ldr, const void* weight, int plus_one, float eps,
                     int64_t M, int64_t K, int dtype, void* out, int64_t ldo, uint8_t* q, int64_t ldq, float* scales,
                     hipStream_t stream);
@@ -107,7 +108,7 @@ static int check_weights(const char* who, int64_t N, int64_t K, int scale_fmt, c
 
 extern "C" {
 
-int w4a8_abi_version(void) { return 2; }
+int w4a8_abi_version(void) { return 3; }
 
 const char* w4a8_last_error(void) { return g_err; }
 
@@ -523,6 +524,55 @@ int w4a8_moe_gemm2_combine(const void* a, int a_dtype, int64_t lda, const int32_
   const int64_t rb = moe_max_blocks(numel, E, block_m, P) * block_m / 16;
   return hip_status(launch_moe_gemm2_combine(p, rb, reinterpret_cast<const uint16_t*>(a), lda, a_dtype, inv_pos,
                                              topk_ids, topk_w, T, (int)E, (hipStream_t)stream), who);
+}
+
+int w4a8_moe_route_gemm1(const void* logits, int logits_dtype, int64_t T, int64_t E, int top_k, int renormalize,
+                         const void* x, int x_dtype, int64_t ldx, int block_m, int64_t P, const void* w_tile, int64_t N,
+                         int64_t K, const void* scales, int scale_fmt, const int32_t* zeros, int wfmt,
+                         int64_t group_size, float* topk_w, int32_t* topk_ids, int32_t* sorted_ids,
+                         int32_t* expert_ids, int32_t* ntp, int32_t* inv_pos, void* out, int out_dtype, int64_t ldo,
+                         void* stream) {
+  const char* who = "w4a8_moe_route_gemm1";
+  if (int rc = check_route(who, logits_dtype, E, top_k)) return rc;
+  if (int rc = check_weights(who, N, K, scale_fmt, zeros, wfmt, group_size)) return rc;
+  if (T < 0) return fail(kErrInvalid, "%s: T=%lld negative", who, (long long)T);
+  const int64_t numel = T * top_k;
+  if (int rc = check_align(who, numel, E, block_m, P)) return rc;
+  if (x_dtype != kBF16 && x_dtype != kF16) return fail(kErrInvalid, "%s: x must be bf16 or fp16", who);
+  if (K % 8 || ldx < K || ldx % 8 || !aligned16(x))
+    return fail(kErrInvalid, "%s: x rows must be 16-byte aligned with stride >= K (K=%lld ldx=%lld)", who,
+                (long long)K, (long long)ldx);
+  if (out_dtype != kBF16 && out_dtype != kF16) return fail(kErrInvalid, "%s: the gemm1 buffer must be bf16 or fp16", who);
+  if (N % 32 || ldo < N / 2) return fail(kErrInvalid, "%s: N=%lld must be a multiple of 32, ldo >= N/2", who, (long long)N);
+  if (!topk_w || !topk_ids || !sorted_ids || !expert_ids || !ntp || !inv_pos || !out)
+    return fail(kErrInvalid, "%s: every route output and the gemm1 buffer are required", who);
+  // one 16-row block per slot (block_m < 64), the slots within the capacity and no more than the
+  // experts (the grouped gemm2 sizes its grid for numel / block_m + min(E, numel) blocks), experts
+  // within the in-kernel router's reach
+  if (block_m >= 64 || numel * block_m > P || numel > E || E > kRouteMaxExperts || numel > 64)
+    return fail(kErrUnsupported, "%s: %lld slots, E=%lld, block_m=%d take the route + slots launch", who,
+                (long long)numel, (long long)E, block_m);
+  if (numel == 0) return kOk;
+  GemmArgs p = {};
+  p.xsrc = reinterpret_cast<const uint16_t*>(x); p.ldxs = ldx; p.xdtype = x_dtype; p.M = P;
+  p.N = N; p.K = K; p.KT = (K + 127) / 128;
+  p.wt = reinterpret_cast<const uint4*>(w_tile);
+  p.scales = scales; p.sfmt = scale_fmt; p.zeros = zeros; p.group = (int)group_size; p.wfmt = wfmt;
+  p.sorted_ids = sorted_ids;  // non-null marks the grouped plan; the routed kernel writes it, reads none
+  p.top_k = top_k; p.num_slots = numel; p.bm = block_m; p.a_by_token = 1;
+  p.w_expert_tiles = (N / 16) * p.KT;
+  p.s_expert_stride = (K / group_size) * N;
+  p.z_expert_stride = scale_fmt == kScaleE4M3 ? N : (K / group_size) * (N / 8);
+  p.logits = logits; p.ldtype = logits_dtype; p.num_experts = (int)E; p.renorm = renormalize;
+  p.tw_out = topk_w; p.ids_out = topk_ids; p.inv_out = inv_pos; p.sorted_out = sorted_ids; p.eid_out = expert_ids;
+  p.ntp_out = ntp;
+  p.out = out; p.out_dtype = out_dtype; p.ldo = ldo; p.silu = 1;
+  const int64_t rb = moe_max_blocks(numel, E, block_m, P) * block_m / 16;
+  const int rc = launch_moe_route_gemm1(p, rb, (hipStream_t)stream);
+  if (rc == kErrUnsupported)
+    return fail(kErrUnsupported, "%s: formats %d/%d, group %lld, K=%lld take the route + slots launch", who, wfmt,
+                scale_fmt, (long long)group_size, (long long)K);
+  return hip_status(rc, who);
 }
 
 int w4a8_moe_combine(const void* y, int y_dtype, int64_t ldy, const int32_t* inv_pos, const float* topk_w, int64_t T,

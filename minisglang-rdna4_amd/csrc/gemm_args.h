@@ -4,6 +4,9 @@
 
 namespace w4a8 {
 
+// most experts the routed decode GEMV's in-kernel router covers (four per lane of a wave)
+constexpr int kRouteMaxExperts = 256;
+
 struct GemmArgs {
   // activations: fp8 rows (row stride ldx bytes) + per-row f32 scale
   const uint8_t* xq;
@@ -35,6 +38,18 @@ struct GemmArgs {
   int64_t w_expert_tiles;  // tiles per expert
   int64_t s_expert_stride; // scale elements per expert
   int64_t z_expert_stride; // zero words per expert
+  // routed decode GEMV (kARoute): router logits (T, num_experts) and the route it writes, per slot
+  // the weight, expert and padded row, per 16-row block the sorted ids and the owner, and ntp
+  const void* logits;
+  int ldtype;
+  int num_experts;
+  int renorm;
+  float* tw_out;
+  int32_t* ids_out;
+  int32_t* inv_out;
+  int32_t* sorted_out;
+  int32_t* eid_out;
+  int32_t* ntp_out;
   // output
   void* out;
   int out_dtype;

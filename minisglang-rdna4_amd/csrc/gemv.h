@@ -18,6 +18,7 @@
 // through LDS in a fixed order: results do not depend on timing, and no second kernel is needed.
 #pragma once
 #include "gemm_args.h"
+#include "moe_route.h"
 
 
 namespace w4a8 {
@@ -158,7 +159,14 @@ constexpr int kModeI4 = 0, kModeI4Sub = 1, kModeE8M0 = 2, kModeE2M1F16 = 3, kMod
 //   kAStage:  fp8 rows copied once per workgroup into LDS.
 //   kAQuant:  bf16/fp16 rows read once per workgroup, quantized per token (the act-quant kernel's
 //             arithmetic, bit for bit) into LDS.
-constexpr int kAGlobal = 0, kAStage = 1, kAQuant = 2;
+//   kARoute:  kAQuant for gemm1 of a decode-sized MoE batch, one slot per workgroup row block
+//             (blockIdx.z = slot, output row slot * bm): the workgroup routes the slot's token
+//             itself (moe_route.h, on the logits in p.logits), takes the slot's expert and
+//             quantizes the token's row; strip group 0 of each token's first slot writes the route
+//             (weights, ids, inverse positions, sorted ids, block owners, ntp) as the route + slot
+//             launch would, so the batch needs no launch before gemm1.
+constexpr int kAGlobal = 0, kAStage = 1, kAQuant = 2, kARoute = 3;
+constexpr int kRoutePer = kRouteMaxExperts / 64;  // experts per lane of the in-kernel router
 constexpr int kStageMax = 8;                // most 16-byte staging loads per thread (SM <= this)
 
 // When a wave issues its first window of weight loads (compile-time, so that the compiler's wait
@@ -197,6 +205,8 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemmArgs p, int tpw) {
   static_assert(AF != kWinAFirst || AMODE == kAQuant, "A-first applies to the fused quant");
   static_assert(AF != kWinWaitAll || AMODE == kAStage, "wait-all applies to fp8 staging");
   constexpr bool kStaged = AMODE != kAGlobal;
+  constexpr bool kRoute = AMODE == kARoute;
+  constexpr bool kQuant = AMODE == kAQuant || kRoute;  // bf16/fp16 rows quantized in the prologue
   // grouped (MoE) rows only reach the global-A kernels: the staged and fused kernels are compiled
   // without the align lookups, so their prologue has no chain of dependent argument loads
   constexpr bool kMayGroup = AMODE == kAGlobal;
@@ -219,7 +229,11 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemmArgs p, int tpw) {
                  "s"(p.s_expert_stride), "s"(p.z_expert_stride));
   }
   const int64_t sg = xcd_remap((int)blockIdx.x, (int)gridDim.x);
-  const int64_t m0 = (int64_t)blockIdx.z * 16;
+  // routed: the block is slot blockIdx.z (output row slot * bm), its A row the slot's token
+  const int64_t m0 = kRoute ? (int64_t)blockIdx.z * p.bm : (int64_t)blockIdx.z * 16;
+  const int64_t tok = kRoute ? (int64_t)blockIdx.z / p.top_k : 0;
+  uint32_t logit_raw[kRoute ? kRoutePer : 1];
+  if constexpr (kRoute) route_load<kRoutePer>(p.logits, p.ldtype, tok, p.num_experts, logit_raw);
 
   int64_t expert = 0;
   if (kMayGroup && p.sorted_ids) {
@@ -229,10 +243,10 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemmArgs p, int tpw) {
   // A row of this lane. A row that holds no data reads row 0 instead: an A row only feeds its
   // own output row, which is never stored, and a valid address keeps the loads branch-free.
   int64_t ar = m0 + (lane & 15);
-  const bool row_ok = kMayGroup ? row_source(p, m0 + (lane & 15), ar) : ar < p.M;
+  bool row_ok = kRoute ? (lane & 15) == 0 : kMayGroup ? row_source(p, m0 + (lane & 15), ar) : ar < p.M;
   const uint8_t* arow = p.xq + (row_ok ? ar : 0) * p.ldx;
   // act scale of the row, loaded now so the epilogue does not wait on a dependent load
-  float row_scale = (AMODE != kAQuant && row_ok) ? p.act_scales[ar] : 0.f;
+  float row_scale = (!kQuant && row_ok) ? p.act_scales[ar] : 0.f;
 
   const int64_t nstrips = p.N / kTileN;
   const int half = p.silu ? NSTR / 2 : NSTR;
@@ -241,12 +255,6 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemmArgs p, int tpw) {
 #pragma unroll
   for (int j = 0; j < NSTR; ++j) sval[j] = strip_of(p.silu, sg, j, half, NSTR, nstrips, strip[j]);
 
-  const uint4* wt = p.wt + (size_t)(expert * p.w_expert_tiles) * 64;
-  // scale element size from the mode (E8M0 bytes, else fp16), so that the scale base stays in
-  // scalar registers
-  const int kEsz = (MODE == kModeE8M0 || MODE == kModeNV || (MODE == kModeE2M1F16 && p.sfmt == kScaleE4M3)) ? 1 : 2;
-  const void* scales = reinterpret_cast<const char*>(p.scales) + (size_t)(expert * p.s_expert_stride) * kEsz;
-  const int32_t* zeros = p.zeros ? p.zeros + expert * p.z_expert_stride : nullptr;
   // 32-bit index math on the hot path (tile, scale and zero indices of one matrix fit easily)
   const int N = (int)p.N, K = (int)p.K, KT = (int)p.KT;
   const int gshift = 31 - __builtin_clz((unsigned)(p.group >= kTileK ? p.group / kTileK : 1));  // tiles per group
@@ -254,14 +262,15 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemmArgs p, int tpw) {
 
   // ---- A staging loads, issued before any weight load so that waiting for them never waits for
   // weights. Rows [0, rv) of the block; each row padded with zeros to whole tiles.
-  const int rv = kStaged ? (int)(p.M - m0 < 16 ? p.M - m0 : 16) : 0;
+  const int rv = kRoute ? 1 : kStaged ? (int)(p.M - m0 < 16 ? p.M - m0 : 16) : 0;
+  const int64_t xr0 = kRoute ? tok : m0;  // source row of the block's row 0
   const int lstride = stage_stride(KT);
   unsigned char* a_lds = smem;
-  constexpr int kEl = AMODE == kAQuant ? 8 : 16;  // elements per 16-byte load
-  const int cpr = KT * (kTileK / kEl);            // loads per padded row
+  constexpr int kEl = kQuant ? 8 : 16;  // elements per 16-byte load
+  const int cpr = KT * (kTileK / kEl);  // loads per padded row
   const int nchunks = rv * cpr;
   uint4 stg[kStaged ? SM : 1];
-  if (kStaged) {
+  auto issue_stage = [&]() {
 #pragma unroll
     for (int i = 0; i < SM; ++i) {
       int c = (int)threadIdx.x + i * (int)blockDim.x;
@@ -269,12 +278,57 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemmArgs p, int tpw) {
       const int r = c / cpr;
       int k = (c - r * cpr) * kEl;
       k = k < K ? k : K - kEl;  // padding: any valid address, the value is replaced by zeros
-      if (AMODE == kAQuant)
-        stg[i] = *reinterpret_cast<const uint4*>(p.xsrc + (m0 + r) * p.ldxs + k);
+      if (kQuant)
+        stg[i] = *reinterpret_cast<const uint4*>(p.xsrc + (xr0 + r) * p.ldxs + k);
       else
-        stg[i] = *reinterpret_cast<const uint4*>(p.xq + (m0 + r) * p.ldx + k);
+        stg[i] = *reinterpret_cast<const uint4*>(p.xq + (xr0 + r) * p.ldx + k);
+    }
+  };
+  if constexpr (kRoute) {
+    // the row's loads go out behind the logits' and ahead of the route, whose wait for the
+    // logits leaves them in flight
+    issue_stage();
+    // the slot's choice needs the first jj + 1 rounds; the wave that writes the route, all top_k
+    const int jj = (int)((int64_t)blockIdx.z - tok * p.top_k);
+    const bool writer = blockIdx.x == 0 && wave == 0 && jj == 0;
+    const RoutePick rp = route_pick<kRoutePer>(logit_raw, p.ldtype, p.num_experts, writer ? p.top_k : jj + 1);
+    const int e = __builtin_amdgcn_readlane(rp.myid, jj);
+    const bool eok = e >= 0 && e < p.num_experts;
+    // a slot left without an expert (NaN logits) is dropped: no output row, expert E-1's
+    // weights for valid addresses
+    expert = eok ? e : p.num_experts - 1;
+    row_ok = row_ok && eok;
+    if (writer) {
+      // the token's route, written once: per slot s the weight, the expert, the padded row; the
+      // slot's block holds s in its first row and the sentinel S in the others
+      float mx, sum;
+      route_softmax<kRoutePer>(logit_raw, p.ldtype, p.num_experts, mx, sum);
+      const float w = route_weight(rp, mx, sum, p.top_k, p.renorm);
+      const int S = (int)p.num_slots, bm = p.bm;
+      const int64_t s0 = tok * p.top_k;
+      const bool mine_ok = rp.myid >= 0 && rp.myid < p.num_experts;
+      if (lane < p.top_k) {
+        p.tw_out[s0 + lane] = w;
+        p.ids_out[s0 + lane] = rp.myid;
+        p.inv_out[s0 + lane] = mine_ok ? (int32_t)((s0 + lane) * bm) : -1;
+        p.eid_out[s0 + lane] = mine_ok ? rp.myid : p.num_experts - 1;
+      }
+      for (int j = 0; j < p.top_k; ++j) {
+        const int ej = __builtin_amdgcn_readlane(rp.myid, j);
+        const bool ok = ej >= 0 && ej < p.num_experts;
+        if (lane < bm) p.sorted_out[(s0 + j) * bm + lane] = (lane == 0 && ok) ? (int32_t)(s0 + j) : S;
+      }
+      if (tok == 0 && lane == 0) *p.ntp_out = S * bm;
     }
   }
+
+  const uint4* wt = p.wt + (size_t)(expert * p.w_expert_tiles) * 64;
+  // scale element size from the mode (E8M0 bytes, else fp16), so that the scale base stays in
+  // scalar registers
+  const int kEsz = (MODE == kModeE8M0 || MODE == kModeNV || (MODE == kModeE2M1F16 && p.sfmt == kScaleE4M3)) ? 1 : 2;
+  const void* scales = reinterpret_cast<const char*>(p.scales) + (size_t)(expert * p.s_expert_stride) * kEsz;
+  const int32_t* zeros = p.zeros ? p.zeros + expert * p.z_expert_stride : nullptr;
+  if (kStaged && !kRoute) issue_stage();
 
   const int kt_begin = wave * tpw;
   const int kt_last = kt_begin + tpw < KT ? kt_begin + tpw : KT;
@@ -349,7 +403,7 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemmArgs p, int tpw) {
     for (int t = 0; t < CH; ++t) load_tile(t, clamp_kt(kt_begin + t));
   }
 
-  if (AMODE == kAQuant) {
+  if (kQuant) {
     // per-row amax: lane r (< 16) of each wave ends with the wave's maximum of row r
     float rowmax = 0.f;
     if (rv == 1) {
@@ -516,7 +570,7 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemmArgs p, int tpw) {
   // Cross-wave reduction through LDS, over the block's existing rows only (row i = 4q + r of the
   // C fragment lives in lane 16q + c, element r): a one-row decode call moves 16 floats per wave.
   float* red = reinterpret_cast<float*>(smem + (kStaged ? ((rv * lstride + 15) / 16) * 16 : 0));
-  const int nr = (kMayGroup && p.sorted_ids) ? 16 : (int)(p.M - m0 < 16 ? p.M - m0 : 16);
+  const int nr = kRoute ? 1 : (kMayGroup && p.sorted_ids) ? 16 : (int)(p.M - m0 < 16 ? p.M - m0 : 16);
   if (wave == 0 && lane < 16) {
     srow[lane] = row_scale;
     rvalid[lane] = row_ok ? 1 : 0;
@@ -585,6 +639,10 @@ bool launch_gemv_fused_e2m1(const GemmArgs& p, dim3 grid, const GemvPlan& pl, hi
 bool launch_gemv_generic(const GemmArgs& p, dim3 grid, const GemvPlan& pl, hipStream_t stream);
 // K split (waves, tiles per wave) the GEMV runs for these arguments and row blocks
 void gemv_ksplit(const GemmArgs& p, int64_t row_blocks, int& waves, int& tpw);
+// the planner itself (quant_src: p.xsrc holds bf16/fp16 rows the kernel may quantize)
+GemvPlan plan_gemv(const GemmArgs& p, int64_t row_blocks, bool quant_src);
+// gemm1 of a decode-sized MoE batch with the router in the prologue (gemv_routed.hip)
+int launch_moe_route_gemm1(const GemmArgs& p, int64_t row_blocks, hipStream_t stream);
 
 // NVFP4 (e2m1 weights, e4m3 group-16 scales, per-channel global): the fast path's dedicated mode
 inline bool gemv_nvfp4(const GemmArgs& p) {

@@ -15,6 +15,7 @@
 #include <cstdlib>
 
 #include "act_quant.h"
+#include "moe_route.h"
 
 namespace w4a8 {
 
@@ -23,100 +24,6 @@ constexpr int kMaxExperts = 512;
 __device__ __forceinline__ float load_logit(const void* p, int dtype, int64_t i) {
   if (dtype == kF32) return reinterpret_cast<const float*>(p)[i];
   return from_dtype(reinterpret_cast<const uint16_t*>(p)[i], dtype);
-}
-
-// (value, expert) argmax step against the DPP partner: larger logit, then lower expert index
-__device__ __forceinline__ bool beats(float ov, int oi, float bv, int bi) {
-  return (ov > bv) | ((ov == bv) & (oi < bi));  // non-short-circuit: selects, not branches
-}
-template <int CTRL>
-__device__ __forceinline__ void argmax_step(float& bv, int& bi) {
-  const float ov = dpp_f<CTRL>(bv);
-  const int oi = dpp_i<CTRL>(bi);
-  const bool take = beats(ov, oi, bv, bi);
-  bv = take ? ov : bv;
-  bi = take ? oi : bi;
-}
-
-// Route of token t by one wave (all 64 lanes active): lane l holds experts l + 64*i, i < PER.
-// Softmax over the f32-widened logits (max, then the sum of exp in a fixed tree order), top-k by
-// repeated wave argmax on the logits (which orders the experts exactly as the probabilities do;
-// ties keep the lower index), then renormalisation by the selected probabilities' sum, taken in
-// selection order, + 1e-8. Writes the k weights and ids to global memory and the ids to ids_s
-// (LDS, optional).
-template <int PER>
-__device__ __forceinline__ void route_token(const void* __restrict__ logits, int dtype, int64_t t, int E,
-                                            int top_k, int renorm, float* __restrict__ tw,
-                                            int32_t* __restrict__ ids, int32_t* ids_s) {
-  const int lane = threadIdx.x & 63;
-  // every load is issued before the first use, whatever the dtype
-  uint32_t raw[PER];
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int e = lane + 64 * i;
-    const int64_t idx = t * E + (e < E ? e : 0);
-    raw[i] = dtype == kF32 ? __float_as_uint(reinterpret_cast<const float*>(logits)[idx])
-                           : (uint32_t)reinterpret_cast<const uint16_t*>(logits)[idx];
-  }
-  float v[PER];
-  float mx = -INFINITY;
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int e = lane + 64 * i;
-    v[i] = e >= E ? -INFINITY : dtype == kF32 ? __uint_as_float(raw[i]) : from_dtype((uint16_t)raw[i], dtype);
-    mx = fmaxf(mx, v[i]);
-  }
-  mx = wave_max(mx);
-  float part = 0.f;
-#pragma unroll
-  for (int i = 0; i < PER; ++i)
-    if (lane + 64 * i < E) part += expf(v[i] - mx);
-  const float sum = wave_sum(part);
-
-  unsigned used = 0;  // bit i: expert lane + 64*i taken
-  float myv = -INFINITY;
-  int myid = 0;
-  for (int j = 0; j < top_k; ++j) {
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int e = lane + 64 * i;
-      const bool take = (e < E) & !((used >> i) & 1u) & beats(v[i], e, bv, bi);
-      bv = take ? v[i] : bv;
-      bi = take ? e : bi;
-    }
-    argmax_step<kDppXor1>(bv, bi);
-    argmax_step<kDppXor2>(bv, bi);
-    argmax_step<kDppHalfMirror>(bv, bi);
-    argmax_step<kDppRowMirror>(bv, bi);
-    // rows 0..3 each hold their argmax in every lane; combine them in scalar registers
-    float cv = lane_f(bv, 0);
-    int ci = __builtin_amdgcn_readlane(bi, 0);
-#pragma unroll
-    for (int r = 1; r < 4; ++r) {
-      const float ov = lane_f(bv, 16 * r);
-      const int oi = __builtin_amdgcn_readlane(bi, 16 * r);
-      const bool take = beats(ov, oi, cv, ci);
-      cv = take ? ov : cv;
-      ci = take ? oi : ci;
-    }
-    bv = cv;
-    bi = ci;
-    if ((bi & 63) == lane) used |= 1u << (bi >> 6);
-    if (lane == j) {
-      myv = bv;
-      myid = bi;
-    }
-  }
-  const float p = lane < top_k ? expf(myv - mx) / sum : 0.f;
-  float wsum = 0.f;
-  for (int j = 0; j < top_k; ++j) wsum += lane_f(p, j);
-  if (lane < top_k) {
-    tw[t * top_k + lane] = renorm ? p / (wsum + 1e-8f) : p;
-    ids[t * top_k + lane] = myid;
-    if (ids_s) ids_s[t * top_k + lane] = myid;
-  }
 }
 
 template <int PER>
@@ -496,10 +403,14 @@ moe_prep_kernel(const void* __restrict__ logits, int ldtype, int64_t T, int E, i
   lds_barrier();
   if (slots) {
     const int S = (int)(T * top_k);
-    for (int i = threadIdx.x; i < S * bm; i += kPrepThreads) sorted_ids[i] = i % bm == 0 ? i / bm : S;
+    // a slot left without an expert (NaN logits leave none to choose) is dropped, as the align
+    // drops it: sentinel rows only, a valid block owner for the weight addresses, inv_pos -1
+    auto eok = [&](int s) { return ids_s[s] >= 0 && ids_s[s] < E; };
+    for (int i = threadIdx.x; i < S * bm; i += kPrepThreads) sorted_ids[i] = (i % bm == 0 && eok(i / bm)) ? i / bm : S;
     if (threadIdx.x < S) {
-      expert_ids[threadIdx.x] = ids_s[threadIdx.x];
-      inv_pos[threadIdx.x] = (int32_t)threadIdx.x * bm;
+      const bool ok = eok(threadIdx.x);
+      expert_ids[threadIdx.x] = ok ? ids_s[threadIdx.x] : E - 1;
+      inv_pos[threadIdx.x] = ok ? (int32_t)threadIdx.x * bm : -1;
     }
     if (threadIdx.x == 0) *ntp = S * bm;
     return;

@@ -50,6 +50,10 @@ _MOE_SKINNY_MAX_ROWS = 40
 # 8 47.6/50.3, 12 60.7/59.9, 16 75.4/68.9 -- so up to 8 tokens.
 _MOE_G2FUSE = os.environ.get("MINISGL_MOE_G2FUSE", "1") != "0"
 _MOE_G2C_MAX_TOKENS = 8
+# route, slots, the per-token quant of x and gemm1 as one launch for the calls that give every slot
+# a block (w4a8_moe_route_gemm1); MINISGL_MOE_ROUTED=0 keeps the route + slots launch and gemm1,
+# which give the same bits
+_MOE_ROUTED = os.environ.get("MINISGL_MOE_ROUTED", "1") != "0"
 
 
 # --------------------------------------------------------------------------------------------
@@ -549,6 +553,41 @@ def _route_align_quant(gating_output: torch.Tensor, top_k: int, renormalize: boo
     return tw, ids, sorted_ids, expert_ids, ntp, inv, xq, xs
 
 
+def _route_gemm1(gating_output, top_k, renormalize, E, block_m, x, t13, N1, w13s, s13f, w13z, wfmt, group):
+    """w4a8_moe_route_gemm1: route + one block per slot + gemm1 with the silu epilogue of a
+    decode-sized batch in one launch, every gemm1 workgroup routing its slot's token itself.
+    Returns (tw, ids, sorted_ids, expert_ids, ntp, inv_pos, gemm1 buffer), the same tensors and
+    bits as w4a8_moe_route_slots followed by the grouped gemm1, or None where the library does not
+    cover the call (formats, sizes); nothing is launched then."""
+    g = gating_output.contiguous()
+    if g.dim() != 2 or g.shape[1] != E:
+        raise AssertionError(f"moe route: gating_output must be (M, E={E}), got {tuple(g.shape)}")
+    xc = x if x.stride(-1) == 1 else x.contiguous()
+    T, K = xc.shape
+    numel = T * top_k
+    lib = _abi.load()
+    P = int(lib.w4a8_moe_padded_capacity(numel, E, block_m))
+    if numel > E or numel * block_m > P:
+        return None
+    dev = g.device
+    tw = torch.empty((T, top_k), dtype=torch.float32, device=dev)
+    ids = torch.empty((T, top_k), dtype=torch.int32, device=dev)
+    sorted_ids = torch.empty((P,), dtype=torch.int32, device=dev)
+    expert_ids = torch.empty(((P + block_m - 1) // block_m,), dtype=torch.int32, device=dev)
+    ntp = torch.empty((1,), dtype=torch.int32, device=dev)
+    inv = torch.empty((max(numel, 1),), dtype=torch.int32, device=dev)
+    buf2 = torch.empty((P, N1 // 2), dtype=xc.dtype, device=dev)
+    rc = lib.w4a8_moe_route_gemm1(
+        _abi.ptr(g), _abi.dtype_code(g.dtype), T, E, top_k, int(bool(renormalize)), _abi.ptr(xc),
+        _abi.dtype_code(xc.dtype), xc.stride(0), block_m, P, _abi.ptr(t13), N1, K, _abi.ptr(w13s), s13f, _abi.ptr(w13z),
+        wfmt, group, _abi.ptr(tw), _abi.ptr(ids), _abi.ptr(sorted_ids), _abi.ptr(expert_ids), _abi.ptr(ntp),
+        _abi.ptr(inv), _abi.ptr(buf2), _abi.dtype_code(xc.dtype), N1 // 2, _abi.stream_of(xc))
+    if rc == _abi.ERR_UNSUPPORTED:
+        return None
+    _abi.check(rc, "w4a8_moe route_gemm1")
+    return tw, ids, sorted_ids, expert_ids, ntp, inv, buf2
+
+
 def _moe_route(gating_output: torch.Tensor, top_k: int, renormalize: bool, num_experts: int):
     engaged("w4a8_mi355x.moe_route_align")
     g = gating_output.contiguous()
@@ -720,30 +759,6 @@ def _moe_forward(x, w13, w13_scales, w13_zeros, w2, w2_scales, w2_zeros, gating_
             f"{tuple(act_scales.shape)}")
     elif act_scales is not None:
         raise AssertionError("w4a8_moe: act_scales given without x_fp8")
-    xq = xs = None
-    if topk_ids is None:
-        # route + align, and the per-token quant of x unless the producer supplied it (one launch
-        # for small batches); the align's inverse positions (slot -> padded row) feed the combine.
-        # Up to _MOE_SLOTS_MAX tokens on the decode arm: one block per slot instead of the align
-        # (one token's experts are distinct, so the align would share no block either; a few tokens
-        # share few, and a shared expert's weights are then streamed once per slot). configs[4],
-        # whole call, align -> slots: T=1 23.9 -> 21.1 us, T=2 28.5 -> 25.6, T=4 34.3 -> 31.0,
-        # T=8 50.9 -> 47.8; T=16 68.8 -> 79.0, so the align stays from there on
-        topk_weights, topk_ids, sorted_ids, expert_ids, ntp, inv, xq, xs = _route_align_quant(
-            gating_output, top_k, renormalize, E, block_m, x if x_fp8 is None else None,
-            slots=M <= _MOE_SLOTS_MAX and block_m < 64)
-    else:
-        assert topk_weights is not None, "topk_weights required when topk_ids is given"
-        topk_weights = topk_weights.to(torch.float32).contiguous()
-        topk_ids = topk_ids.to(torch.int32).contiguous()
-        engaged("w4a8_mi355x.moe_align")
-        sorted_ids, expert_ids, ntp, inv = _moe_align(topk_ids, E, block_m)
-    P = sorted_ids.shape[0]
-    numel = topk_ids.numel()
-    if x_fp8 is not None:
-        xq, xs = _fp8_bytes(x_fp8).contiguous(), act_scales.to(torch.float32).contiguous()
-    elif xq is None:
-        xq, xs = act_quant(x)
 
     wfmt = _abi.W_E2M1 if weight_is_e2m1 else _abi.W_INT4
     t13 = _as_tiles(w13, K, weight_is_e2m1, 3, "w4a8_moe w13")
@@ -754,15 +769,50 @@ def _moe_forward(x, w13, w13_scales, w13_zeros, w2, w2_scales, w2_zeros, gating_
         w13_scales = w13_scales.view(torch.uint8)
     if s2f == _abi.SCALE_E4M3:
         w2_scales = w2_scales.view(torch.uint8)
+    w13s = w13_scales.contiguous()
+    w13z = w13_zeros.contiguous() if w13_zeros is not None else None
     arm = _abi.KERNEL_DECODE if block_m < 64 else _abi.KERNEL_PREFILL
     arm_name = "gemv" if arm == _abi.KERNEL_DECODE else "mfma"
     e2 = "+e2m1" if weight_is_e2m1 else ""
 
-    buf2 = torch.empty((P, inter), dtype=x.dtype, device=x.device)
-    engaged(f"w4a8_mi355x.moe_gemm1_silu({arm_name}{e2}{'+prequant' if x_fp8 is not None else ''})")
-    _moe_gemm(xq, K, xs, 1, sorted_ids, expert_ids, ntp, numel, top_k, block_m, P, t13, E, N1, K,
-              w13_scales.contiguous(), s13f, w13_zeros.contiguous() if w13_zeros is not None else None, wfmt, _grp,
-              buf2, _abi.dtype_code(x.dtype), inter, True, arm, "w4a8_moe gemm1")
+    # Up to _MOE_SLOTS_MAX tokens on the decode arm: one block per slot instead of the align (one
+    # token's experts are distinct, so the align would share no block either; a few tokens share
+    # few, and a shared expert's weights are then streamed once per slot). configs[4], whole call,
+    # align -> slots: T=1 23.9 -> 21.1 us, T=2 28.5 -> 25.6, T=4 34.3 -> 31.0, T=8 50.9 -> 47.8;
+    # T=16 68.8 -> 79.0, so the align stays from there on
+    slots = M <= _MOE_SLOTS_MAX and block_m < 64
+    buf2 = None
+    if topk_ids is None and x_fp8 is None and slots and _MOE_ROUTED:
+        # route, slots, the per-token quant of x and gemm1 in one launch (same bits as below)
+        r = _route_gemm1(gating_output, top_k, renormalize, E, block_m, x, t13, N1, w13s, s13f, w13z, wfmt, _grp)
+        if r is not None:
+            topk_weights, topk_ids, sorted_ids, expert_ids, ntp, inv, buf2 = r
+            engaged(f"w4a8_mi355x.moe_route_gemm1_silu(gemv{e2})")
+    if buf2 is None:
+        xq = xs = None
+        if topk_ids is None:
+            # route + align (or slots), and the per-token quant of x unless the producer supplied
+            # it (one launch for small batches); the inverse positions (slot -> padded row) feed
+            # the combine
+            topk_weights, topk_ids, sorted_ids, expert_ids, ntp, inv, xq, xs = _route_align_quant(
+                gating_output, top_k, renormalize, E, block_m, x if x_fp8 is None else None, slots=slots)
+        else:
+            assert topk_weights is not None, "topk_weights required when topk_ids is given"
+            topk_weights = topk_weights.to(torch.float32).contiguous()
+            topk_ids = topk_ids.to(torch.int32).contiguous()
+            engaged("w4a8_mi355x.moe_align")
+            sorted_ids, expert_ids, ntp, inv = _moe_align(topk_ids, E, block_m)
+        if x_fp8 is not None:
+            xq, xs = _fp8_bytes(x_fp8).contiguous(), act_scales.to(torch.float32).contiguous()
+        elif xq is None:
+            xq, xs = act_quant(x)
+        P = sorted_ids.shape[0]
+        buf2 = torch.empty((P, inter), dtype=x.dtype, device=x.device)
+        engaged(f"w4a8_mi355x.moe_gemm1_silu({arm_name}{e2}{'+prequant' if x_fp8 is not None else ''})")
+        _moe_gemm(xq, K, xs, 1, sorted_ids, expert_ids, ntp, topk_ids.numel(), top_k, block_m, P, t13, E, N1, K,
+                  w13s, s13f, w13z, wfmt, _grp, buf2, _abi.dtype_code(x.dtype), inter, True, arm, "w4a8_moe gemm1")
+    P = sorted_ids.shape[0]
+    numel = topk_ids.numel()
 
     lib = _abi.load()
     w2s = w2_scales.contiguous()

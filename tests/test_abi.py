@@ -70,7 +70,7 @@ def test_library_exports_every_declared_symbol(lib):
     raw = ctypes.CDLL(str(pkg("_abi").lib_path()))
     for name in _declared():
         assert hasattr(raw, name), f"{name} declared in {HEADER.name} but not exported"
-    assert lib.w4a8_abi_version() == 2
+    assert lib.w4a8_abi_version() == 3
 
 
 def test_host_validation_rejects_before_launch(lib):

@@ -57,7 +57,7 @@ def test_route_align_bit_exact(kernels, oracle, dev, T):
 
 
 @pytest.mark.parametrize("T", [1, 3, 8])
-def test_route_slots_layout(kernels, oracle, dev, T):
+def test_route_slots_layout(kernels, oracle, dev, monkeypatch, T):
     """w4a8_moe_route_slots (w4a8_moe's routing for decode batches): the route and x's codes equal
     the align path's bit for bit; slot s owns padded row s*bm of a block of its own (the other rows
     sentinels), its block's owner is its expert, inv_pos[s] = s*bm, ntp = slots*bm; and w4a8_moe on
@@ -89,6 +89,7 @@ def test_route_slots_layout(kernels, oracle, dev, T):
     w13, s13, _ = synth.int4_weight(2 * I, H, G, seed=905, asym=False, E=E, scale_floor=1e-3)
     w2, s2, _ = synth.int4_weight(H, I, G, seed=906, asym=False, E=E, scale_floor=1e-3)
     before = eng.counts()
+    monkeypatch.setattr(kernels, "_MOE_ROUTED", False)  # the two-launch arm (the routed one: below)
     res = kernels._moe_forward(x, w13.to(dev), s13.to(dev), None, w2.to(dev), s2.to(dev), None, lg.to(dev), TOPK,
                                True)
     _sync()
@@ -385,6 +386,73 @@ def test_moe_fused_gemm2_combine_bit_exact(kernels, dev, monkeypatch, fmt, T, bm
         for f in fused:
             dmax = (f["out"].float() - plain["out"].float()).abs().max().item()
             assert torch.equal(f["out"], plain["out"]), f"{fmt} T={T} bm={bm}: fused differs, max|d| {dmax:.3e}"
+
+
+@pytest.mark.parametrize("fmt", ["sym", "asym", "mxfp4", "nvfp4"])
+@pytest.mark.parametrize("T,e,k,bm,ldt", [(1, 128, 8, 16, torch.float32), (3, 64, 6, 16, torch.bfloat16),
+                                          (8, 256, 8, 16, torch.float32), (2, 40, 4, 32, torch.float16)])
+def test_moe_routed_gemm1_bit_exact(kernels, dev, monkeypatch, fmt, T, e, k, bm, ldt):
+    """Route + slots + gemm1 in one launch (w4a8_moe_route_gemm1: the router runs in every gemm1
+    workgroup) gives the bits of the route + slots launch followed by the grouped gemm1: routing
+    weights and ids, inverse positions, the slot blocks below ntp and their owners, ntp, the gemm1
+    rows of the slots and the MoE output. E = 40 leaves lanes of the router without an expert, 256
+    fills all four per lane; both renormalize arms; f32, bf16 and fp16 logits."""
+    h, i = 1024, 768
+    w13, s13, z13, w2, s2, z2, e2 = _fmt_experts(fmt, e, h, i, seed=610 + T)
+    d = lambda t: None if t is None else t.to(dev)
+    t13 = kernels.repack_w4(w13.to(dev), weight_is_e2m1=e2)
+    t2 = kernels.repack_w4(w2.to(dev), weight_is_e2m1=e2)
+    args = (t13, d(s13), d(z13), t2, d(s2), d(z2))
+    x = synth.activations(T, h, seed=620 + T).to(dev)
+    lg = synth.router_logits(T, e, seed=621 + T, dtype=ldt).to(dev)
+    renorm = T % 2 == 1
+    eng = pkg("_hip_engage")
+    res = {}
+    for routed in (True, False):
+        monkeypatch.setattr(kernels, "_MOE_ROUTED", routed)
+        before = eng.counts()
+        res[routed] = kernels._moe_forward(x, *args, lg, k, renorm, block_m=bm, weight_is_e2m1=e2)
+        _sync()
+        took = eng.counts_delta(before)
+        assert (took.get(f"w4a8_mi355x.moe_route_gemm1_silu(gemv{'+e2m1' if e2 else ''})", 0) == 1) == routed, took
+    a, b = res[True], res[False]
+    S = T * k
+    for key in ("topk_weights", "topk_ids", "ntp"):
+        assert torch.equal(a[key], b[key]), key
+    assert int(a["ntp"].item()) == S * bm
+    assert torch.equal(a["inv_pos"][:S], b["inv_pos"][:S])
+    assert torch.equal(a["sorted_ids"][: S * bm], b["sorted_ids"][: S * bm])
+    assert torch.equal(a["expert_ids"][:S], b["expert_ids"][:S])
+    rows = b["inv_pos"][:S].long()
+    assert torch.equal(a["buf2"][rows], b["buf2"][rows]), f"{fmt} T={T}: gemm1 rows differ"
+    assert torch.equal(a["out"], b["out"]), f"{fmt} T={T}: output differs"
+
+
+def test_moe_routed_gemm1_nan_logits_drop_slots(kernels, dev, monkeypatch):
+    """A token whose logits are all NaN has no expert to choose: both decode routings (in-kernel
+    and the route + slots launch) drop its slots (inv_pos -1, sentinel blocks owned by a valid
+    expert), so its output is zero and the other token's output is unchanged."""
+    e, k, h, i = 64, 4, 1024, 768
+    w13, s13, z13, w2, s2, z2, e2 = _fmt_experts("sym", e, h, i, seed=640)
+    args = (kernels.repack_w4(w13.to(dev)), s13.to(dev), None, kernels.repack_w4(w2.to(dev)), s2.to(dev), None)
+    x = synth.activations(2, h, seed=641).to(dev)
+    lg_ok = synth.router_logits(2, e, seed=642, dtype=torch.float32)
+    lg = lg_ok.clone()
+    lg[1] = float("nan")
+    lg, lg_ok = lg.to(dev), lg_ok.to(dev)
+    res = {}
+    for routed in (True, False):
+        monkeypatch.setattr(kernels, "_MOE_ROUTED", routed)
+        res[routed] = kernels._moe_forward(x, *args, lg, k, True, block_m=16)
+    one = kernels._moe_forward(x, *args, lg_ok, k, True, block_m=16)  # token 0's output, same batch shape
+    _sync()
+    for routed, r in res.items():
+        inv = r["inv_pos"][: 2 * k].cpu()
+        assert (inv[k:] == -1).all() and (inv[:k] >= 0).all(), (routed, inv)
+        assert (r["expert_ids"][: 2 * k].cpu() < e).all()
+        assert torch.equal(r["out"][1], torch.zeros_like(r["out"][1])), routed
+        assert torch.equal(r["out"][0], one["out"][0]), routed
+    assert torch.equal(res[True]["out"], res[False]["out"])
 
 
 # ------------------------------------------------------------------------------- W4A16 expert arm
