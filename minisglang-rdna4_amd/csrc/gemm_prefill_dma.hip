@@ -57,13 +57,25 @@ gemm_dma_kernel(const GemmArgs p) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave / WN, wn = wave % WN;
-  const int64_t blk_row0 = (int64_t)blockIdx.y * BM;
-
+  int bx = (int)blockIdx.x, by = (int)blockIdx.y;
   int64_t expert = 0;
   if (p.sorted_ids) {
-    if (blk_row0 >= (int64_t)(*p.ntp)) return;
-    expert = p.expert_ids[blk_row0 / p.bm];
+    // Grouped: tiles in XCD order. Workgroup i runs on XCD i % 8; each XCD takes a contiguous
+    // range of the tiles that hold rows (row tiles below ntp, every column tile of each), so a
+    // row tile's A rows and an expert's weight strips, read by the neighbouring tiles, stay in one
+    // L2 (in grid order a row tile's column tiles and an expert's row tiles sat on different XCDs).
+    // The grid is a multiple of 8 workgroups, so every XCD has the same number of slots.
+    const int gx = (int)gridDim.x;
+    const int i = by * gx + bx;
+    const int used = ((*p.ntp) + BM - 1) / BM * gx;
+    const int share = (used + 7) / 8;
+    const int v = (i & 7) * share + (i >> 3);
+    if ((i >> 3) >= share || v >= used) return;
+    bx = v % gx;
+    by = v / gx;
+    expert = p.expert_ids[(int64_t)by * BM / p.bm];
   }
+  const int64_t blk_row0 = (int64_t)by * BM;
   const int N = (int)p.N, K = (int)p.K, KT = (int)p.KT;
   const int nstrips = N / kTileN;
   const int gshift = 31 - __builtin_clz((unsigned)(p.group >= kTileK ? p.group / kTileK : 1));
@@ -75,11 +87,11 @@ gemm_dma_kernel(const GemmArgs p) {
     if (p.silu) {
       constexpr int hj = NSB / 2;
       const int j = s % NSB;
-      const int h = (int)blockIdx.x * (NSTRIP / 2) + (s / NSB) * hj + (j < hj ? j : j - hj);
+      const int h = bx * (NSTRIP / 2) + (s / NSB) * hj + (j < hj ? j : j - hj);
       gs = j < hj ? h : nstrips / 2 + h;
       ok = h < nstrips / 2;
     } else {
-      gs = (int)blockIdx.x * NSTRIP + s;
+      gs = bx * NSTRIP + s;
       ok = gs < nstrips;
     }
     return ok ? gs : nstrips - 1;
@@ -372,7 +384,11 @@ static int launch_dma_cfg(const GemmArgs& p, int64_t row_tiles, hipStream_t stre
   constexpr int BN = WN * NSB * 16;
   const int64_t ncols = p.silu ? p.N / 2 : p.N;
   const int64_t colw = p.silu ? BN / 2 : BN;
-  const dim3 grid((unsigned)((ncols + colw - 1) / colw), (unsigned)row_tiles);
+  const int64_t gx = (ncols + colw - 1) / colw;
+  int64_t gy = row_tiles;
+  if (p.sorted_ids)  // the grouped tile order needs a multiple of 8 workgroups
+    while ((gx * gy) % 8) ++gy;
+  const dim3 grid((unsigned)gx, (unsigned)gy);
   const dim3 block(WM * WN * 64);
   auto kern = gemm_dma_kernel<WM, WN, RB, NSB, MODE>;
   hipLaunchKernelGGL(kern, grid, block, 0, stream, p);
