@@ -118,6 +118,21 @@ gemm_dma_kernel(const GemmArgs p) {
     const bool ok = lrow_source(p, blk_row0 + (b >> 1) * 16 + (lane & 15), ar);
     a_voff[i] = (uint32_t)((ok ? ar : 0) * p.ldx) + (b & 1) * 64 + 16 * (lane >> 4);
   }
+  // The epilogue's rows: one per thread, its source looked up in the same round trip as the A
+  // rows' and its act scale loaded ahead of step 0's loads; both go to LDS at the end of the
+  // prologue, so the epilogue starts with no load to wait for (grouped rows had three dependent
+  // ones there: ntp, sorted id, act scale). LDS rather than registers: the int4 tiles already use
+  // nearly every VGPR through the K loop.
+  __shared__ float e_sc[BM];
+  __shared__ int e_ok[BM];
+  const int er = (int)threadIdx.x;
+  float er_sc = 0.f;
+  bool er_ok = false;
+  if (er < BM) {
+    int64_t ar;
+    er_ok = lrow_source(p, blk_row0 + er, ar);
+    er_sc = p.act_scales[er_ok ? ar : 0];
+  }
   // fp4: wave strip s = wave + i*NW; E8M0 dword of DMA lane m (< 16): 32-block m >> 2, channels
   // 4 * (m & 3) .. +3 (LDS byte (m >> 2) * 16 + channel = the MFMA lane whose scale it is)
   int b_gs[kFp4 ? B_DMA : 1];
@@ -350,11 +365,17 @@ gemm_dma_kernel(const GemmArgs p) {
     __builtin_amdgcn_s_barrier();
   };
 
-  // prologue: steps 0 and 1 in flight, step 0 in LDS
+  // prologue: steps 0 and 1 in flight, step 0 in LDS. The epilogue rows' loads above are older
+  // than both, so the counted wait covers them; their LDS writes land before the first step's
+  // barrier (its wait takes lgkmcnt to 0), long before the epilogue reads them.
   issue(IC<0>{}, 0);
   issue(IC<1>{}, 1);
   commit(IC<0>{}, IC<0>{});
   wait_vm_lgkm0<NOPS>();
+  if (er < BM) {
+    e_sc[er] = er_sc;
+    e_ok[er] = er_ok ? 1 : 0;
+  }
   __builtin_amdgcn_s_barrier();
   int kt = 0;
   for (; kt + 4 < KT; kt += 3) {
@@ -370,13 +391,23 @@ gemm_dma_kernel(const GemmArgs p) {
 
   // epilogue: lane holds rows 4*(lane>>4)+r of each row block, channel (lane & 15) of each strip
   const int64_t row0 = blk_row0 + (int64_t)wm * RB * 16;
+  float e_rsc[RB][4];
+  uint32_t e_valid = 0;
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int lr = wm * RB * 16 + rb * 16 + 4 * (lane >> 4) + r;
+      e_rsc[rb][r] = e_sc[lr];
+      e_valid |= (e_ok[lr] ? 1u : 0u) << (rb * 4 + r);
+    }
   // the stages are free: the last step's barrier followed every wave's reads and every DMA
   constexpr int kScr = 16 * (NSB * 16 * 4 + 16);  // one wave's row-major tile, f32 worst case
   constexpr int kWps = kStage / kScr;
   static_assert(3 * kWps >= NW, "epilogue scratch");
   unsigned char* scr = (wave < kWps ? st0 : wave < 2 * kWps ? st1 : st2) + (wave % kWps) * kScr;
-  store_tile(p, acc, row0, lane, [&](int j, bool& ok) __attribute__((always_inline)) { return gstrip(wn * NSB + j, ok); },
-             scr);
+  store_tile_scaled(p, acc, e_rsc, e_valid, row0, lane,
+                    [&](int j, bool& ok) __attribute__((always_inline)) { return gstrip(wn * NSB + j, ok); }, scr);
 }
 
 template <int WM, int WN, int RB, int NSB, int MODE>

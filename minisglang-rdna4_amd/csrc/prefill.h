@@ -157,21 +157,36 @@ __device__ __forceinline__ void store_tile_lds(const GemmArgs& p, const v4f (&ac
 // vector-memory counter covers both), which serialized the whole epilogue.
 // scr (may be null): this wave's LDS scratch for the row-major store path, at least
 // 16 * (NSB*16*4 + 16) bytes, free to overwrite.
-template <int RB, int NSB, typename SF>
-__device__ __forceinline__ void store_tile(const GemmArgs& p, const v4f (&acc)[RB][NSB], int64_t row0, int lane,
-                                           SF strip, unsigned char* scr = nullptr) {
+// The epilogue rows' sources, split from their scales so a kernel can look them up early (with
+// its A rows) and load the scales behind its first loads: bit rb*4+r of the result is set when the
+// lane's row row0 + rb*16 + 4*(lane>>4) + r holds data, ar[rb][r] its activation row.
+template <int RB>
+__device__ __forceinline__ uint32_t tile_row_sources(const GemmArgs& p, int64_t row0, int lane, int64_t (&ar)[RB][4]) {
   static_assert(RB * 4 <= 32, "row mask");
-  float sc[RB][4];
   uint32_t valid = 0;
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      int64_t ar;
-      const bool ok = lrow_source(p, row0 + rb * 16 + 4 * (lane >> 4) + r, ar);
-      sc[rb][r] = p.act_scales[ok ? ar : 0];
+      const bool ok = lrow_source(p, row0 + rb * 16 + 4 * (lane >> 4) + r, ar[rb][r]);
       valid |= (ok ? 1u : 0u) << (rb * 4 + r);
     }
+  return valid;
+}
+template <int RB>
+__device__ __forceinline__ void tile_row_scales(const GemmArgs& p, const int64_t (&ar)[RB][4], uint32_t valid,
+                                                float (&sc)[RB][4]) {
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sc[rb][r] = p.act_scales[((valid >> (rb * 4 + r)) & 1u) ? ar[rb][r] : 0];
+}
+
+// The epilogue with the rows' scales and validity already in registers.
+template <int RB, int NSB, typename SF>
+__device__ __forceinline__ void store_tile_scaled(const GemmArgs& p, const v4f (&acc)[RB][NSB], const float (&sc)[RB][4],
+                                                  uint32_t valid, int64_t row0, int lane, SF strip,
+                                                  unsigned char* scr = nullptr) {
   const int esz = p.out_dtype == kF32 ? 4 : 2;
   if (scr && ((reinterpret_cast<uintptr_t>(p.out) | (uintptr_t)(p.ldo * esz)) & 15) == 0) {
     // the wave's strips are consecutive columns; count those inside N
@@ -206,6 +221,16 @@ __device__ __forceinline__ void store_tile(const GemmArgs& p, const v4f (&acc)[R
   } else {
     store_tile_dt<kF32, false>(p, acc, sc, valid, row0, lane, strip);
   }
+}
+
+template <int RB, int NSB, typename SF>
+__device__ __forceinline__ void store_tile(const GemmArgs& p, const v4f (&acc)[RB][NSB], int64_t row0, int lane,
+                                           SF strip, unsigned char* scr = nullptr) {
+  int64_t ar[RB][4];
+  const uint32_t valid = tile_row_sources<RB>(p, row0, lane, ar);
+  float sc[RB][4];
+  tile_row_scales<RB>(p, ar, valid, sc);
+  store_tile_scaled(p, acc, sc, valid, row0, lane, strip, scr);
 }
 
 // Launch of the DMA-staged kernel (gemm_prefill_dma.hip); kErrUnsupported when it does not apply.
