@@ -28,6 +28,9 @@ int launch_moe_align(const int32_t* ids, int64_t numel, int E, int bm, int64_t P
 int launch_moe_combine(const void* y, int ydt, int64_t ldy, const int32_t* inv_pos, const float* tw, int64_t T,
                        int top_k, int64_t H, void* out, int dtype, hipStream_t stream);
 bool moe_prep_fits(int64_t T, int top_k);
+int launch_moe_route_quant(const void* logits, int ldtype, int64_t T, int E, int top_k, int renorm, float* tw,
+                           int32_t* ids, const void* x, int xdtype, int64_t K, int64_t ldx, uint8_t* xq, int64_t ldq,
+                           float* xs, hipStream_t stream);
 int launch_moe_route_gemm1(const GemmArgs& p, int64_t row_blocks, hipStream_t stream);
 int launch_rms_norm(const void* x, int64_t ldx, void* res, int64_t ldr, const void* weight, int plus_one, float eps,
                     int64_t M, int64_t K, int dtype, void* out, int64_t ldo, uint8_t* q, int64_t ldq, float* scales,
@@ -393,9 +396,14 @@ int w4a8_moe_route_align(const void* logits, int logits_dtype, int64_t T, int64_
     return hip_status(launch_moe_prep(logits, logits_dtype, T, (int)E, top_k, renormalize, topk_w, topk_ids, block_m, P,
                                       sorted_ids, expert_ids, ntp, inv_pos, x, x_dtype, K, ldx, x_fp8, ldq, x_scales,
                                       0, st), "moe_route_align");
-  int rc = launch_moe_route(logits, logits_dtype, T, (int)E, top_k, renormalize, topk_w, topk_ids, st);
+  // route and the quant of x in one launch where the rows allow it, then the align
+  int rc = x ? launch_moe_route_quant(logits, logits_dtype, T, (int)E, top_k, renormalize, topk_w, topk_ids, x, x_dtype,
+                                      K, ldx, x_fp8, ldq, x_scales, st)
+             : kErrUnsupported;
+  const bool quantized = rc == kOk && x;
+  if (rc == kErrUnsupported) rc = launch_moe_route(logits, logits_dtype, T, (int)E, top_k, renormalize, topk_w, topk_ids, st);
   if (!rc) rc = launch_moe_align(topk_ids, T * top_k, (int)E, block_m, P, sorted_ids, expert_ids, ntp, inv_pos, st);
-  if (!rc && x) rc = launch_act_quant(x, x_dtype, T, K, ldx, x_fp8, ldq, x_scales, nullptr, st);
+  if (!rc && x && !quantized) rc = launch_act_quant(x, x_dtype, T, K, ldx, x_fp8, ldq, x_scales, nullptr, st);
   return hip_status(rc, "moe_route_align");
 }
 

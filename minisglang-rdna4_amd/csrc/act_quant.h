@@ -25,6 +25,35 @@ __device__ __forceinline__ float block_max(float v, float* red) {
   return v;
 }
 
+// One row (K <= CPW*512) quantized by one wave: CPW 16-byte loads per lane, all issued before the
+// first use, the maximum by wave_max alone (no LDS, no barrier). Same arithmetic as quant_row, bit
+// for bit. All 64 lanes active.
+template <int CPW>
+__device__ __forceinline__ void quant_row_wave(const uint16_t* __restrict__ xr, int64_t K, int dtype,
+                                               uint8_t* __restrict__ qr, float* __restrict__ scale_out, int lane) {
+  uint4 raw[CPW];
+#pragma unroll
+  for (int c = 0; c < CPW; ++c) {
+    const int64_t k = ((int64_t)c * 64 + lane) * 8;
+    raw[c] = k < K ? *reinterpret_cast<const uint4*>(xr + k) : make_uint4(0, 0, 0, 0);
+  }
+  float amax = 0.f;
+#pragma unroll
+  for (int c = 0; c < CPW; ++c) amax = fmaxf(amax, amax8(raw[c], dtype));
+  const float s = act_row_scale(wave_max(amax));
+  const float inv = 1.0f / s;
+#pragma unroll
+  for (int c = 0; c < CPW; ++c) {
+    const int64_t k = ((int64_t)c * 64 + lane) * 8;
+    if (k < K) {
+      float f[8];
+      unpack8(raw[c], dtype, f);
+      *reinterpret_cast<uint2*>(qr + k) = quant8(f, inv);
+    }
+  }
+  if (lane == 0) *scale_out = s;
+}
+
 // One row quantized by a workgroup of NT threads, 8 elements per thread per pass. CPT > 0: the row
 // (<= NT*8*CPT elements) is read once into registers. CPT == 0: two passes.
 template <int CPT, int NT = kAqThreads>

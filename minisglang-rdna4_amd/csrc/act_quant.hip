@@ -43,30 +43,8 @@ act_quant_wave_kernel(const uint16_t* __restrict__ x, int64_t ldx, int64_t M, in
     rows = rc < M ? rc : M;
   }
   const int64_t stride = (int64_t)gridDim.x * (blockDim.x >> 6);
-  for (int64_t m = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); m < rows; m += stride) {
-    const uint16_t* xr = x + m * ldx;
-    uint4 raw[CPW];
-#pragma unroll
-    for (int c = 0; c < CPW; ++c) {
-      const int64_t k = ((int64_t)c * 64 + lane) * 8;
-      raw[c] = k < K ? *reinterpret_cast<const uint4*>(xr + k) : make_uint4(0, 0, 0, 0);
-    }
-    float amax = 0.f;
-#pragma unroll
-    for (int c = 0; c < CPW; ++c) amax = fmaxf(amax, amax8(raw[c], dtype));
-    const float s = act_row_scale(wave_max(amax));
-    const float inv = 1.0f / s;
-#pragma unroll
-    for (int c = 0; c < CPW; ++c) {
-      const int64_t k = ((int64_t)c * 64 + lane) * 8;
-      if (k < K) {
-        float f[8];
-        unpack8(raw[c], dtype, f);
-        *reinterpret_cast<uint2*>(q + m * ldq + k) = quant8(f, inv);
-      }
-    }
-    if (lane == 0) scales[m] = s;
-  }
+  for (int64_t m = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); m < rows; m += stride)
+    quant_row_wave<CPW>(x + m * ldx, K, dtype, q + m * ldq, scales + m, lane);
 }
 
 int launch_act_quant(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx, uint8_t* q,

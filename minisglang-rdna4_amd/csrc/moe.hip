@@ -427,6 +427,27 @@ moe_prep_kernel(const void* __restrict__ logits, int ldtype, int64_t T, int E, i
   align_block<kPrepThreads, 64 * PER, 0>(ids_s, T * top_k, E, bm, P, sorted_ids, expert_ids, ntp, inv_pos);
 }
 
+// Route of T tokens and the per-token quant of x in one launch, for batches past the one-launch
+// prep (more than 256 slots) with rows the wave quant covers (K <= 4096): workgroups
+// [0, route_blocks) route four tokens each (a wave per token, route_token), the rest quantize four
+// rows each (a wave per row, quant_row_wave: the act-quant kernel's arithmetic). The halves share
+// nothing, so they run side by side where they were two launches; the align follows it.
+template <int PER, int CPW>
+__global__ void __launch_bounds__(256)
+moe_route_quant_kernel(const void* __restrict__ logits, int ldtype, int64_t T, int E, int top_k, int renorm,
+                       float* __restrict__ tw, int32_t* __restrict__ ids, int64_t route_blocks,
+                       const uint16_t* __restrict__ x, int xdtype, int64_t K, int64_t ldx, uint8_t* __restrict__ xq,
+                       int64_t ldq, float* __restrict__ xs) {
+  const int64_t w = threadIdx.x >> 6;  // whole waves leave together below
+  if ((int64_t)blockIdx.x < route_blocks) {
+    const int64_t t = (int64_t)blockIdx.x * 4 + w;
+    if (t < T) route_token<PER>(logits, ldtype, t, E, top_k, renorm, tw, ids, nullptr);
+    return;
+  }
+  const int64_t m = ((int64_t)blockIdx.x - route_blocks) * 4 + w;
+  if (m < T) quant_row_wave<CPW>(x + m * ldx, K, xdtype, xq + m * ldq, xs + m, threadIdx.x & 63);
+}
+
 // Four channels per thread: 16-byte (f32 y) or 8-byte (bf16/fp16 y) loads of y, one 8-byte (or
 // 16-byte f32) store. YF32: y holds f32 rows; else rows in ydt (bf16/fp16), widened exactly.
 template <bool YF32>
@@ -537,6 +558,35 @@ template <int PER> struct PrepLaunch {
 #undef W4A8_PREP
   }
 };
+
+template <int PER> struct RouteQuantLaunch {
+  static void run(int cpw, const void* logits, int ldtype, int64_t T, int E, int top_k, int renorm, float* tw,
+                  int32_t* ids, const uint16_t* x, int xdtype, int64_t K, int64_t ldx, uint8_t* xq, int64_t ldq,
+                  float* xs, hipStream_t stream) {
+    const int64_t rb = (T + 3) / 4;
+    const dim3 grid((unsigned)(2 * rb));
+#define W4A8_RQ(C) hipLaunchKernelGGL((moe_route_quant_kernel<PER, C>), grid, dim3(256), 0, stream, logits, ldtype, T, E, \
+                                      top_k, renorm, tw, ids, rb, x, xdtype, K, ldx, xq, ldq, xs)
+    if (cpw <= 1) W4A8_RQ(1);
+    else if (cpw <= 2) W4A8_RQ(2);
+    else if (cpw <= 4) W4A8_RQ(4);
+    else W4A8_RQ(8);
+#undef W4A8_RQ
+  }
+};
+
+// Route + per-token quant of x as one launch (rows of K <= 4096 elements); kErrUnsupported for
+// longer rows, which take the route and act-quant kernels.
+int launch_moe_route_quant(const void* logits, int ldtype, int64_t T, int E, int top_k, int renorm, float* tw,
+                           int32_t* ids, const void* x, int xdtype, int64_t K, int64_t ldx, uint8_t* xq, int64_t ldq,
+                           float* xs, hipStream_t stream) {
+  if (T <= 0) return kOk;
+  if (K > 64 * 8 * 8 || T > (int64_t)1 << 30) return kErrUnsupported;
+  const int cpw = (int)((K + 511) / 512);
+  with_per<RouteQuantLaunch>(E, cpw, logits, ldtype, T, E, top_k, renorm, tw, ids,
+                             reinterpret_cast<const uint16_t*>(x), xdtype, K, ldx, xq, ldq, xs, stream);
+  return hipGetLastError() == hipSuccess ? kOk : kErrHip;
+}
 
 bool moe_prep_fits(int64_t T, int top_k) { return T * top_k <= kPrepMaxSlots; }
 
