@@ -1,7 +1,8 @@
 // Skinny-M W4A8 GEMM (decode band, up to 16 rows per row block) on the 16x16x128 f8f6f4 MFMA:
 // the kernel template, shared by the launch units gemm_decode.hip (A read per tile from global
-// memory), gemv_staged.hip (fp8 A staged in LDS) and gemv_fused.hip (bf16/fp16 A quantized to fp8
-// in LDS by the kernel itself, so a decode call is one launch).
+// memory), gemv_staged.hip (fp8 A staged in LDS), gemv_fused.hip and gemv_fused_e2m1.hip (bf16/fp16
+// A quantized to fp8 in LDS by the kernel itself, so a decode call is one launch), gemv_generic.hip
+// (sub-tile groups) and gemv_routed.hip (MoE gemm1 with the router in the prologue).
 //
 // Restates the math of the reference's decode_gemv arm of mmq_fp8_gemm
 // (python/minisgl/quant/kernels.py:1562-1563, 1686-1734) and of its fused gate_up+silu twin
