@@ -117,7 +117,9 @@ int w4a8_moe_route(const void* logits, int logits_dtype, int64_t T, int64_t E, i
  * with the outputs of w4a8_moe_route and w4a8_moe_align (numel = T*top_k). When x is non-NULL it also
  * quantizes x (T, K) per token into x_fp8 / x_scales, as w4a8_act_quant does (the act-quant the grouped
  * gemm1 needs, kernels.py:1703-1712). Up to 256 slots (T*top_k) run as a single launch: one workgroup
- * routes and aligns while the others quantize the token rows. */
+ * routes and aligns while the others quantize the token rows. Past that, rows of K <= 4096 are
+ * quantized in the routing launch (a wave per token routes, a wave per row quantizes) and the align
+ * follows: two launches. */
 int w4a8_moe_route_align(const void* logits, int logits_dtype, int64_t T, int64_t E, int top_k, int renormalize,
                          int block_m, int64_t P, float* topk_w, int32_t* topk_ids, int32_t* sorted_ids,
                          int32_t* expert_ids, int32_t* ntp, int32_t* inv_pos, const void* x, int x_dtype, int64_t K,
