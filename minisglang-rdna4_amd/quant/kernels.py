@@ -41,7 +41,9 @@ _MOE_GEMM1_GEMV_MAX = 32
 _MOE_WMMA_DIM = 16
 _MOE_BLOCK_M_CHOICES = (16, 32, 64, 128)
 # routed rows per expert up to which w4a8_moe runs the skinny grouped GEMV (block_m 16)
-_MOE_SKINNY_MAX_ROWS = 40
+_MOE_SKINNY_MAX_ROWS = 32
+# and 64-row MFMA tiles up to this many, 128-row tiles above
+_MOE_MID_MAX_ROWS = 44
 # gemm2 + top-k combine as one launch on the decode arm (python/minisgl/quant/kernels.py:831-850)
 # up to _MOE_G2C_MAX_TOKENS tokens; MINISGL_MOE_G2FUSE=0 keeps the unfused path (requant, gemm2
 # into (P, H) f32, combine), which gives the same bits. The fused kernel reads each routed expert's
@@ -489,16 +491,23 @@ def _moe_block_m(num_tokens: int, num_experts: int, top_k: int, flag_gemm1: bool
 
 def _moe_block_m_auto(num_tokens: int, num_experts: int, top_k: int) -> int:
     """The tile height w4a8_moe picks when the caller gives none, from MI355X measurements of these
-    kernels at the configs[4] shape (E=128, top-8, H=2048, I=768): the skinny grouped GEMV (16-row
-    blocks) up to 40 routed rows per expert, where it streams each expert's weights once per 16
-    rows (T=256: 124 us, against 203 us with the 64-row tiles the reference's rule picks there);
-    128-row MFMA tiles above (T=1024: 263 us, against 320 us at 64). The reference raises to 64
-    past 32 tokens because its own GEMV arm loses there (``_moe_block_m``, kept as written for
-    callers and tests that want that rule). ``MINISGL_MOE_BLOCK_M`` still forces a value."""
+    kernels at the configs[4] shape (E=128, top-8, H=2048, I=768), whole call, us:
+    - the skinny grouped GEMV (16-row blocks) up to 32 routed rows per expert, where it streams
+      each expert's weights once per 16 rows (T=256: 121, against 173 with 64-row tiles and 194
+      with 128; T=512, 32 rows: 178 against 180 and 197);
+    - 64-row MFMA tiles up to 44 rows (T=640, 40 rows: 177, against 205 with the GEMV and 192
+      with 128-row tiles);
+    - 128-row tiles above (T=768: 195 against 197 at 64; T=1024: 200 against 252; T=4096: 502
+      against 738).
+    The reference raises to 64 past 32 tokens because its own GEMV arm loses there
+    (``_moe_block_m``, kept as written for callers and tests that want that rule).
+    ``MINISGL_MOE_BLOCK_M`` still forces a value."""
     if os.environ.get("MINISGL_MOE_BLOCK_M"):
         return _moe_block_m(num_tokens, num_experts, top_k)
     rows_per_expert = (num_tokens * top_k) / max(num_experts, 1)
-    return 16 if rows_per_expert <= _MOE_SKINNY_MAX_ROWS else 128
+    if rows_per_expert <= _MOE_SKINNY_MAX_ROWS:
+        return 16
+    return 64 if rows_per_expert <= _MOE_MID_MAX_ROWS else 128
 
 
 def _route_align(gating_output: torch.Tensor, top_k: int, renormalize: bool, num_experts: int,

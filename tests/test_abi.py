@@ -178,11 +178,12 @@ def test_moe_block_m_policy():
 
 
 def test_moe_block_m_auto_policy(monkeypatch):
-    """w4a8_moe's own choice: 16-row GEMV blocks up to 40 routed rows per expert, 128-row tiles above;
-    MINISGL_MOE_BLOCK_M forces a value as in the reference."""
+    """w4a8_moe's own choice: 16-row GEMV blocks up to 32 routed rows per expert, 64-row tiles up to
+    44, 128-row tiles above; MINISGL_MOE_BLOCK_M forces a value as in the reference."""
     auto = pkg("quant.kernels")._moe_block_m_auto
     monkeypatch.delenv("MINISGL_MOE_BLOCK_M", raising=False)
-    assert [auto(T, 128, 8) for T in (1, 16, 256, 512, 1024, 4096)] == [16, 16, 16, 16, 128, 128]
+    assert [auto(T, 128, 8) for T in (1, 16, 256, 512, 576, 640, 704, 768, 1024, 4096)] == \
+        [16, 16, 16, 16, 64, 64, 64, 128, 128, 128]
     assert auto(64, 32, 4) == 16 and auto(2048, 32, 4) == 128
     monkeypatch.setenv("MINISGL_MOE_BLOCK_M", "64")
     assert auto(4096, 128, 8) == 64
