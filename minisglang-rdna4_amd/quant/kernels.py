@@ -49,9 +49,10 @@ _MOE_MID_MAX_ROWS = 44
 # into (P, H) f32, combine), which gives the same bits. The fused kernel reads each routed expert's
 # weights once per token where the grouped gemm2 reads them once per expert; measured on MI355X at
 # configs[4] (whole w4a8_moe call, fused / unfused, us): T=1 25.2/29.5, 2 28.7/33.8, 4 34.0/39.0,
-# 8 47.6/50.3, 12 60.7/59.9, 16 75.4/68.9 -- so up to 8 tokens.
+# 8 47.6/50.3, 12 60.7/59.9, 16 75.4/68.9 at first; with the fused kernel's tile loads all issued
+# before their first use, T=10 49.8/55.3, 12 57.0/62.7, 14 62.8/67.6, 16 66.6/69.4 -- so up to 16.
 _MOE_G2FUSE = os.environ.get("MINISGL_MOE_G2FUSE", "1") != "0"
-_MOE_G2C_MAX_TOKENS = 8
+_MOE_G2C_MAX_TOKENS = 16
 # route, slots, the per-token quant of x and gemm1 as one launch for the calls that give every slot
 # a block (w4a8_moe_route_gemm1); MINISGL_MOE_ROUTED=0 keeps the route + slots launch and gemm1,
 # which give the same bits
