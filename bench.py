@@ -128,8 +128,8 @@ def roofline_leg(kernels, dev, reps: int = 60) -> dict:
         traffic = json.loads(tf.read_text()).get("traffic_bytes_per_launch")
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-            "kernel": "gemv_kernel<4,3,kModeI4,kAQuant,SYM,2,1,kWinAfterA> (decode GEMV, int4 sym g128, fused act quant, 4 strips per workgroup) "
-                      "K=4096 N=28672 M=1",
+            "kernel": "gemv_walk_kernel<1,4,kModeI4,SYM,1,bf16> (strip-walking decode GEMV, int4 sym g128, act quant "
+                      "in the row phase, 256 workgroups of two 4-wave sets) K=4096 N=28672 M=1",
             "algorithmic_bytes_per_launch": nbytes, "mean_launch_us": round(mean_us, 3), "launches": reps}
 
 
@@ -439,9 +439,16 @@ def producer_leg(kernels, dev, weights, steps: int = 100) -> dict:
         torch.cuda.synchronize()
         out[name] = {"us_per_step": round((time.perf_counter() - t0) * 1e6 / steps, 1)}
         del graph, keep
-    out["launches_per_step"] = {"in_op_quant": "20 norms + 14 act-quant + 20 GEMV",
+    aq = launches_per_step() - len(MS) * len(SHAPES)
+    out["launches_per_step"] = {"in_op_quant": f"20 norms + {aq} act-quant + 20 GEMV",
                                 "producer_pair": "20 norms (with the quant epilogue) + 20 GEMV"}
     return out
+
+
+def launches_per_step() -> int:
+    """Kernel launches of one configs[1] step (w4a8_linear_launch_count over its 20 calls)."""
+    lib = importlib.import_module("minisglang-rdna4_amd._abi").load()
+    return sum(lib.w4a8_linear_launch_count(M, N, K, 0, 0, 0, 0, GROUP, 0, 0) for M in MS for (K, N) in SHAPES)
 
 
 def main() -> int:
@@ -559,7 +566,8 @@ def main() -> int:
                 "activations with 0.1% channels x50",
         "config": {
             "workload": "configs[1]: decode W4A8 GEMM sweep at Llama-3-8B layer shapes, M in {1,2,4,8,16}; one step = "
-                        "20 calls (act-quant + GEMM each), HIP-graph replayed",
+                        "20 calls (per-token act quant + GEMM each), HIP-graph replayed",
+            "launches_per_step": launches_per_step(),
             "shapes_KxN": [f"{K}x{N}" for K, N in SHAPES],
             "M": MS,
             "group_size": GROUP,

@@ -41,7 +41,10 @@ extern "C" {
 #define W4A8_SCALE_E8M0 1
 #define W4A8_SCALE_E4M3 2
 
-/* ABI revision (1). */
+/* ABI revision of this header. A client checks w4a8_abi_version() == W4A8_ABI_VERSION at load:
+ * revision 3 inserted y_dtype as w4a8_moe_combine's second argument, revision 4 added
+ * w4a8_linear_launch_count. */
+#define W4A8_ABI_VERSION 4
 int w4a8_abi_version(void);
 
 /* Message of the calling thread's last failed call. */
@@ -85,14 +88,23 @@ int64_t w4a8_linear_workspace_bytes(int64_t M, int64_t K);
 /* Dense W4A8 linear on bf16/fp16 activations x (M, ldx): per-token fp8 quant of x, then the GEMM of
  * w4a8_gemm, with the same outputs bit for bit as w4a8_act_quant followed by w4a8_gemm. This is
  * fp8_wmma.mmq_fp8_gemm / mmq_fp8_gemm_silu called without a producer pair, which quantize in-op
- * (python/minisgl/quant/kernels.py:1686-1753, in-op quant :1703-1712). For decode-sized calls
- * whose rows fit the kernel's LDS (rows x K up to about 16K elements) the quant runs in the GEMV
- * kernel's prologue and the call is a single launch; otherwise one act-quant launch writes the
- * workspace (w4a8_linear_workspace_bytes, 16-byte aligned) first. */
+ * (python/minisgl/quant/kernels.py:1686-1753, in-op quant :1703-1712). Decode calls (M <= 16) whose
+ * rows the GEMV can quantize itself (int4 with groups of 128+ and MXFP4, up to 64 values per thread
+ * of its row phase, 128 on weights of over 64 KiB per workgroup: at K = 4096 up to 8 rows, 16 on
+ * the wide gate_up shape; see w4a8_linear_launch_count) are a single launch; otherwise one act-quant
+ * launch writes the workspace (w4a8_linear_workspace_bytes, 16-byte aligned) first. */
 int w4a8_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const void* w_tile, int64_t N,
                 const void* scales, int scale_fmt, const int32_t* zeros, int wfmt, int64_t group_size, void* out,
                 int out_dtype, int64_t ldo, int silu, void* workspace, int64_t workspace_bytes, int kernel,
                 void* stream);
+
+/* Kernel launches a w4a8_linear call of these shapes and formats makes: 1 when the per-token quant
+ * runs inside the GEMV (decode calls whose rows the GEMV quantizes itself), 2 when an act-quant
+ * launch comes first; 0 for M = 0; minus the status code on bad arguments. Host-only (no device
+ * call), for callers that budget launches per step. No counterpart in the reference, whose in-op
+ * quant is always a separate launch (python/minisgl/quant/kernels.py:1512-1515). */
+int w4a8_linear_launch_count(int64_t M, int64_t N, int64_t K, int x_dtype, int scale_fmt, int has_zeros, int wfmt,
+                             int64_t group_size, int silu, int kernel);
 
 /* w4a8_linear for callers that cannot allocate device memory (code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc). No counterpart in the reference: its ops

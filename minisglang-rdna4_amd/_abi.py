@@ -37,6 +37,8 @@ SIGNATURES = {
     "w4a8_linear_workspace_bytes": (_c_i64, [_c_i64, _c_i64]),
     "w4a8_linear": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _c_i64, _vp, _c_i64, _vp, _c_int, _vp, _c_int, _c_i64,
                              _vp, _c_int, _c_i64, _c_int, _vp, _c_i64, _c_int, _vp]),
+    "w4a8_linear_launch_count": (_c_int, [_c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_i64, _c_int,
+                                          _c_int]),
     "w4a8_linear_noalloc_max_bytes": (_c_i64, []),
     "w4a8_linear_noalloc": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _c_i64, _vp, _c_i64, _vp, _c_int, _vp, _c_int,
                                      _c_i64, _vp, _c_int, _c_i64, _c_int, _c_int, _vp]),

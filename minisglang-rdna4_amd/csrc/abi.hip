@@ -7,6 +7,7 @@
 #include <stdio.h>
 
 #include "gemm_args.h"
+#include "../../include/w4a8_mi355x.h"
 
 namespace w4a8 {
 int launch_act_quant(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx, uint8_t* q,
@@ -111,7 +112,7 @@ static int check_weights(const char* who, int64_t N, int64_t K, int scale_fmt, c
 
 extern "C" {
 
-int w4a8_abi_version(void) { return 3; }
+int w4a8_abi_version(void) { return W4A8_ABI_VERSION; }
 
 const char* w4a8_last_error(void) { return g_err; }
 
@@ -257,6 +258,26 @@ int w4a8_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, c
   p.xq = xq; p.ldx = K; p.act_scales = xs;
   return run_dense("w4a8_linear", p, kernel, st);
 }
+
+extern "C" {
+
+int w4a8_linear_launch_count(int64_t M, int64_t N, int64_t K, int x_dtype, int scale_fmt, int has_zeros, int wfmt,
+                             int64_t group_size, int silu, int kernel) {
+  // the planner reads shapes and formats only: stand-in pointers (aligned, never dereferenced)
+  const void* fake = reinterpret_cast<const void*>(static_cast<uintptr_t>(256));
+  GemmArgs p;
+  int rc = dense_args("w4a8_linear_launch_count", M, fake, N, K, fake, scale_fmt,
+                      has_zeros ? reinterpret_cast<const int32_t*>(fake) : nullptr, wfmt, group_size,
+                      const_cast<void*>(fake), x_dtype, N, silu, kernel, p);
+  if (rc) return -rc;
+  if (x_dtype != kBF16 && x_dtype != kF16) return -fail(kErrInvalid, "w4a8_linear_launch_count: x must be bf16 or fp16");
+  if (M == 0) return 0;
+  const bool decode = kernel == 1 || (kernel == 0 && M <= kGemvMaxRows);
+  p.xsrc = reinterpret_cast<const uint16_t*>(fake); p.ldxs = K; p.xdtype = x_dtype;
+  return decode && gemv_can_fuse_quant(p, (M + 15) / 16) ? 1 : 2;
+}
+
+}  // extern "C"
 
 // ---- W4A16: unquantized bf16/fp16 activations, split exactly into fp8 terms (w4a16.hip)
 static int64_t round16(int64_t b) { return (b + 15) / 16 * 16; }

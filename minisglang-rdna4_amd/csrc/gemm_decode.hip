@@ -103,6 +103,64 @@ GemvPlan plan_gemv(const GemmArgs& p, int64_t row_blocks, bool quant_src) {
   return pl;
 }
 
+// The strip-walking GEMV (gemv_walk.hip) for one row block of bf16/fp16 rows, int4 with groups of
+// 128+ or MXFP4. Its cost over the weight stream is the row phase, where every workgroup quantizes
+// all M x K values, vpt of them per thread. Measured on MI355X against act quant + gemv_kernel
+// (configs[1] shapes, configs[0], configs[5]; outputs equal bit for bit):
+//   * vpt <= 64: the walk is faster at every shape (K=4096 N=4096 M=4 6.0 against 8.2 us, K=4096
+//     N=6144 M=8 8.1 against 9.0, K=14336 N=4096 M=2 10.0 against 11.9, one-row calls too:
+//     K=4096 N=28672 M=1 12.7 against 13.9);
+//   * vpt <= 128 still pays where a workgroup streams more than 64 KiB of weights (K=4096 N=28672
+//     M=16 17.9 against 19.7, K=14336 N=4096 M=4 11.3 against 12.0); on less it ties or loses
+//     (K=4096 N=6144 M=16 9.8 against 9.7);
+//   * above that it loses (K=14336 N=4096 M=8 15.4 against 13.5, K=2560 N=9728 asym M=16 13.8
+//     against 11.5), and one-row calls on wide MXFP4 weights keep the 4-strip fused-quant kernel
+//     (K=8192 N=28672 M=1 22.4 against 23.6).
+// Grid: 256 workgroups (one per CU), two sets of waves where the one-row plan has 4 or fewer waves
+// (twice the weight bytes in flight: K=4096 N=28672 M=1 12.7 against 18.0 us with one set), a
+// window of 4 tiles per wave (8 and 16 measured slower: their loads delay the rows').
+bool plan_gemv_walk(const GemmArgs& p, int64_t row_blocks, WalkPlan& wp) {
+  if (p.sorted_ids || row_blocks != 1 || p.M < 1 || p.M > 16 || !p.xsrc) return false;
+  const bool i4 = p.wfmt == kInt4 && p.group % kTileK == 0;
+  const bool e8 = p.wfmt == kE2M1 && p.sfmt == kScaleE8M0;
+  if (!i4 && !e8) return false;
+  const int64_t KT = p.KT, strips = p.N / kTileN;
+  if (e8 && p.M == 1 && strips >= 1024) return false;
+  int64_t w, tpw;
+  plan_ksplit(KT, strips, w, tpw);  // the one-row plan: the output bits of gemv_kernel's one-row call
+  const int ns = p.silu ? 2 : 1;
+  const int64_t ngroups = p.silu ? strips / 2 : strips;
+  int64_t rp = 1;
+  while (rp < p.M) rp <<= 1;
+  const int64_t G = ngroups < 256 ? ngroups : 256;
+  const int64_t ngmax = (ngroups + G - 1) / G;
+  const int64_t sets = (2 * w <= 8 && ngmax >= 2) ? 2 : 1;
+  // threads per row: the largest power of two that fits (plans of 5-7 waves leave the rest idle in
+  // the row phase)
+  int tpr_log = 0;
+  while ((int64_t)(2 << tpr_log) * rp <= sets * w * 64) ++tpr_log;
+  const int64_t tpr = (int64_t)1 << tpr_log;
+  if (tpr < 16) return false;
+  const int64_t smn = (KT * (kTileK / 8) + tpr - 1) / tpr;
+  if (smn > 32) return false;
+  const int64_t vpt = p.M * KT * kTileK / (tpr * rp);
+  const int64_t wg_weight_bytes = ngmax * ns * KT * kTileBytes;
+  if (vpt > 128 || (vpt > 64 && wg_weight_bytes <= 64 * 1024)) return false;
+  const size_t a_bytes = (size_t)((p.M * stage_stride((int)KT) + 15) / 16) * 16;
+  const size_t red = (size_t)(ngmax * w * ns * p.M * 16 * 4);
+  if (a_bytes + red > (size_t)kWalkLdsMax) return false;
+  wp.grid = (int)G;
+  wp.waves = (int)w;
+  wp.sets = (int)sets;
+  wp.tpw = (int)tpw;
+  wp.ngroups = (int)ngroups;
+  wp.ngmax = (int)ngmax;
+  wp.tpr_log = tpr_log;
+  wp.sm = smn <= 1 ? 1 : smn <= 2 ? 2 : smn <= 4 ? 4 : smn <= 8 ? 8 : smn <= 16 ? 16 : 32;
+  wp.lds = a_bytes + red;
+  return true;
+}
+
 bool launch_gemv_global(const GemmArgs& p, dim3 grid, const GemvPlan& pl, hipStream_t stream) {
   const int ns = p.silu ? 2 * pl.nstr : pl.nstr;
   bool ok = false;
@@ -118,6 +176,11 @@ bool launch_gemv_global(const GemmArgs& p, dim3 grid, const GemvPlan& pl, hipStr
 // padded rows that can hold data). quant_src: p.xsrc holds bf16/fp16 rows; returns kErrUnsupported
 // when the fused quant does not apply (the caller then quantizes first).
 int launch_gemv(GemmArgs p, int64_t row_blocks, bool quant_src, hipStream_t stream) {
+  WalkPlan wp;
+  if (quant_src && plan_gemv_walk(p, row_blocks, wp)) {
+    if (!launch_gemv_walk(p, wp, stream)) return kErrInvalid;
+    return hipGetLastError() == hipSuccess ? kOk : kErrHip;
+  }
   const GemvPlan pl = plan_gemv(p, row_blocks, quant_src);
   if (quant_src && pl.amode != kAQuant) return kErrUnsupported;
   const int64_t nstrips = p.N / kTileN;
@@ -141,6 +204,8 @@ void gemv_ksplit(const GemmArgs& p, int64_t row_blocks, int& waves, int& tpw) {
 
 // True when launch_gemv can quantize bf16/fp16 rows itself for this call.
 bool gemv_can_fuse_quant(const GemmArgs& p, int64_t row_blocks) {
+  WalkPlan wp;
+  if (plan_gemv_walk(p, row_blocks, wp)) return true;
   return plan_gemv(p, row_blocks, true).amode == kAQuant;
 }
 

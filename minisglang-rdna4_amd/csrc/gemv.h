@@ -629,6 +629,35 @@ struct GemvPlan {
   int ch;       // window of the int4 fused-quant kernels (3 or 4 tiles; the other kernels roll 4)
 };
 
+// Launch shape of the strip-walking GEMV (gemv_walk.hip): one row block of bf16/fp16 rows quantized
+// into LDS once per workgroup, `grid` workgroups each walking a contiguous range of the `ngroups`
+// strip groups (a strip, or a gate strip and its up strip), the one-row K split (waves, tpw).
+struct WalkPlan {
+  int grid;
+  int waves;    // the plan's K-split waves (one set)
+  int sets;     // wave sets per workgroup, each walking every sets-th strip group
+  int tpw;
+  int ngroups;
+  int ngmax;    // most strip groups of one workgroup
+  int tpr_log;  // log2 of the threads per row in the row phase
+  int sm;       // 16-byte row loads per thread
+  size_t lds;   // dynamic LDS: the row codes plus the waves' partial sums
+};
+// dynamic LDS a walking launch may use (the kernel's static arrays take the rest of the 160 KiB)
+constexpr int kWalkLdsMax = 160 * 1024 - 512;
+// the walking kernel's own arguments
+struct WalkArgs {
+  int kw;       // K-split waves per set
+  int sets;     // 1 or 2
+  int tpw;
+  int gbase;    // strip groups per workgroup (ngroups / grid) ...
+  int gextra;   // ... plus one for the first ngroups % grid workgroups
+  int tpr_log;
+};
+bool launch_gemv_walk(const GemmArgs& p, const WalkPlan& wp, hipStream_t stream);
+// false when the walking GEMV does not cover the call
+bool plan_gemv_walk(const GemmArgs& p, int64_t row_blocks, WalkPlan& wp);
+
 // Kernel launch of one A source; defined in the unit that instantiates it. `grid` is
 // (strip groups, 1, row blocks); returns false when no kernel matches the call's formats.
 bool launch_gemv_global(const GemmArgs& p, dim3 grid, const GemvPlan& pl, hipStream_t stream);

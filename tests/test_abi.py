@@ -70,7 +70,7 @@ def test_library_exports_every_declared_symbol(lib):
     raw = ctypes.CDLL(str(pkg("_abi").lib_path()))
     for name in _declared():
         assert hasattr(raw, name), f"{name} declared in {HEADER.name} but not exported"
-    assert lib.w4a8_abi_version() == 3
+    assert lib.w4a8_abi_version() == 4
 
 
 def test_host_validation_rejects_before_launch(lib):
@@ -194,3 +194,23 @@ def test_pick_dense_kernel():
     assert pick(1, k=4096) == "decode_gemv" and pick(16, k=4096) == "decode_gemv"
     assert pick(17, k=4096) == "wmma_tiled_tuned" and pick(8, k=4100) == "wmma_tiled_tuned"
     assert pick(16, weight_is_e2m1=True, group_size=32, k=8192) == "decode_gemv"
+
+
+def test_linear_launch_count(lib):
+    """Launches per w4a8_linear call (host-only planner query): the configs[1] step's calls are single
+    launches (the GEMV quantizes its rows) except the two 14336-wide down projections at 8 and 16
+    rows; prefill calls and sub-tile groups take the act-quant launch first."""
+    step = {}
+    for K, N in [(4096, 6144), (4096, 4096), (4096, 28672), (14336, 4096)]:
+        for M in (1, 2, 4, 8, 16):
+            step[(K, N, M)] = lib.w4a8_linear_launch_count(M, N, K, 0, 0, 0, 0, 128, 0, 0)
+    assert all(v in (1, 2) for v in step.values())
+    assert [k for k, v in step.items() if v == 2] == [(4096, 6144, 16), (4096, 4096, 16), (14336, 4096, 8),
+                                                      (14336, 4096, 16)]
+    assert sum(step.values()) == 24
+    assert lib.w4a8_linear_launch_count(0, 4096, 4096, 0, 0, 0, 0, 128, 0, 0) == 0
+    assert lib.w4a8_linear_launch_count(17, 4096, 4096, 0, 0, 0, 0, 128, 0, 0) == 2
+    assert lib.w4a8_linear_launch_count(4, 4096, 4096, 1, 0, 1, 0, 128, 1, 0) == 1
+    assert lib.w4a8_linear_launch_count(4, 4096, 4096, 0, 0, 1, 0, 32, 0, 0) == 2
+    assert lib.w4a8_linear_launch_count(4, 24, 128, 0, 0, 0, 0, 128, 0, 0) == -1
+    assert b"multiple of 16" in lib.w4a8_last_error()

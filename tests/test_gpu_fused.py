@@ -47,16 +47,21 @@ def test_fused_quant_matches_two_launch(kernels, dev, fmt, dtype):
                                          f"{(fused.float() - pair.float()).abs().max().item():.3e}"
 
 
-@pytest.mark.parametrize("M,K", [(1, 4096), (2, 4096), (1, 14336), (1, 2880)])
+def _launches(lib, M, N, K, e2):
+    return lib.w4a8_linear_launch_count(M, N, K, 0, 1 if e2 else 0, 0, int(e2), 32 if e2 else 128, 0, 1)
+
+
+@pytest.mark.parametrize("M,K", [(1, 4096), (2, 4096), (4, 4096), (8, 4096), (1, 14336), (4, 14336), (1, 2880)])
 def test_fused_quant_is_one_launch(kernels, dev, M, K):
-    """One-row decode calls (and two-row calls on narrow weights) quantize in the GEMV and run
-    without a workspace (no act-quant launch): the ABI refuses a null workspace whenever it would
-    need one."""
+    """Decode calls whose rows the GEMV quantizes itself (the one-row fused prologue, or the
+    strip-walking GEMV for up to 16 rows) run without a workspace (no act-quant launch): the ABI
+    refuses a null workspace whenever it would need one, and the planner query agrees."""
     abi = pkg("_abi")
     lib = abi.load()
     N = 128
     fmt = "e2m1" if K % 128 else "sym"
     tiles, s, z, g, e2 = _weights(kernels, dev, fmt, N, K, seed=K)
+    assert _launches(lib, M, N, K, e2) == 1
     x = synth.activations(M, K, seed=M).to(dev)
     out = torch.empty((M, N), dtype=x.dtype, device=dev)
     rc = lib.w4a8_linear(abi.ptr(x), abi.BF16, M, K, K, abi.ptr(tiles), N, abi.ptr(s),
@@ -69,14 +74,16 @@ def test_fused_quant_is_one_launch(kernels, dev, M, K):
     assert torch.equal(out, ref)
 
 
-@pytest.mark.parametrize("M", [4, 16])
-def test_unfused_needs_workspace(kernels, dev, M):
-    """Blocks of 4 or more rows take the act-quant kernel first: without a workspace the call
+@pytest.mark.parametrize("M,K", [(16, 4096), (8, 14336)])
+def test_unfused_needs_workspace(kernels, dev, M, K):
+    """Calls whose row phase would cost the GEMV more than an act-quant launch (16 rows of 4096 on a
+    narrow weight, 8 rows of 14336) take the act-quant kernel first: without a workspace the call
     fails loudly."""
     abi = pkg("_abi")
     lib = abi.load()
-    K, N = 4096, 128
+    N = 128
     tiles, s, z, g, e2 = _weights(kernels, dev, "sym", N, K, seed=5)
+    assert _launches(lib, M, N, K, e2) == 2
     x = synth.activations(M, K, seed=1).to(dev)
     out = torch.empty((M, N), dtype=x.dtype, device=dev)
     rc = lib.w4a8_linear(abi.ptr(x), abi.BF16, M, K, K, abi.ptr(tiles), N, abi.ptr(s), abi.SCALE_F16, None,
