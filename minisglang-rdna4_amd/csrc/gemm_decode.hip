@@ -30,6 +30,9 @@ static void plan_ksplit(int64_t KT, int64_t groups, int64_t& waves, int64_t& tpw
   int64_t w = (KT + 3) / 4;
   if (w > 8) w = 8;
   if (w < 1) w = 1;
+  // a power of two: 4 waves (two walking sets) rather than 5-7 (K=2560 N=9728 M=16 12.7 -> 10.5 us,
+  // M=1 8.5 -> 7.5; K=2816 N=4096 M=1 6.2 -> 5.4 on gemv_kernel)
+  while (w & (w - 1)) --w;
   while (w > 1 && groups * w > 8192 && (KT + w - 1) / w < 8) w = (w + 1) / 2;
   int64_t t = (KT + w - 1) / w;
   w = (KT + t - 1) / t;
@@ -105,20 +108,21 @@ GemvPlan plan_gemv(const GemmArgs& p, int64_t row_blocks, bool quant_src) {
 
 // The strip-walking GEMV (gemv_walk.hip) for one row block of bf16/fp16 rows, int4 with groups of
 // 128+ or MXFP4. Its cost over the weight stream is the row phase, where every workgroup quantizes
-// all M x K values, vpt of them per thread. Measured on MI355X against act quant + gemv_kernel
-// (configs[1] shapes, configs[0], configs[5]; outputs equal bit for bit):
-//   * vpt <= 64: the walk is faster at every shape (K=4096 N=4096 M=4 6.0 against 8.2 us, K=4096
-//     N=6144 M=8 8.1 against 9.0, K=14336 N=4096 M=2 10.0 against 11.9, one-row calls too:
-//     K=4096 N=28672 M=1 12.7 against 13.9);
+// all M x K values, vpt of them per thread of its 8 waves. Measured on MI355X against act quant +
+// gemv_kernel (configs[1] shapes, configs[0], configs[5] and a few odd shapes; outputs equal bit for
+// bit):
+//   * vpt <= 96: the walk is faster or ties at every shape (K=4096 N=4096 M=4 6.0 against 8.2 us,
+//     K=4096 N=6144 M=8 8.1 against 9.0, K=14336 N=4096 M=2 10.0 against 11.9, K=2560 N=9728 asym
+//     M=16 10.5 against 12.7, one-row calls too: K=4096 N=28672 M=1 12.7 against 13.9);
 //   * vpt <= 128 still pays where a workgroup streams more than 64 KiB of weights (K=4096 N=28672
 //     M=16 17.9 against 19.7, K=14336 N=4096 M=4 11.3 against 12.0); on less it ties or loses
-//     (K=4096 N=6144 M=16 9.8 against 9.7);
-//   * above that it loses (K=14336 N=4096 M=8 15.4 against 13.5, K=2560 N=9728 asym M=16 13.8
-//     against 11.5), and one-row calls on wide MXFP4 weights keep the 4-strip fused-quant kernel
-//     (K=8192 N=28672 M=1 22.4 against 23.6).
-// Grid: 256 workgroups (one per CU), two sets of waves where the one-row plan has 4 or fewer waves
-// (twice the weight bytes in flight: K=4096 N=28672 M=1 12.7 against 18.0 us with one set), a
-// window of 4 tiles per wave (8 and 16 measured slower: their loads delay the rows').
+//     (K=4096 N=6144 M=16 10.0 against 9.8);
+//   * above that it loses (K=14336 N=4096 M=8 15.3 against 13.4), and one-row calls on wide MXFP4
+//     weights keep the 4-strip fused-quant kernel (K=8192 N=28672 M=1 22.4 against 23.6).
+// Grid: 256 workgroups (one per CU) of 8 waves: two walking sets where the one-row plan has 4 or
+// fewer waves (twice the weight bytes in flight: K=4096 N=28672 M=1 12.7 against 18.0 us with one
+// set), the rest helper waves of the row phase; a window of 4 tiles per wave (8 and 16 measured
+// slower: their loads delay the rows').
 bool plan_gemv_walk(const GemmArgs& p, int64_t row_blocks, WalkPlan& wp) {
   if (p.sorted_ids || row_blocks != 1 || p.M < 1 || p.M > 16 || !p.xsrc) return false;
   const bool i4 = p.wfmt == kInt4 && p.group % kTileK == 0;
@@ -135,23 +139,26 @@ bool plan_gemv_walk(const GemmArgs& p, int64_t row_blocks, WalkPlan& wp) {
   const int64_t G = ngroups < 256 ? ngroups : 256;
   const int64_t ngmax = (ngroups + G - 1) / G;
   const int64_t sets = (2 * w <= 8 && ngmax >= 2) ? 2 : 1;
-  // threads per row: the largest power of two that fits (plans of 5-7 waves leave the rest idle in
-  // the row phase)
+  // helper waves fill the workgroup to 8 waves for the row phase (K=2560 N=9728 M=16 with one set
+  // of 5 waves: 13.9 -> 11.8 us)
+  const int64_t bw = 8;
+  // threads per row: the largest power of two that fits
   int tpr_log = 0;
-  while ((int64_t)(2 << tpr_log) * rp <= sets * w * 64) ++tpr_log;
+  while ((int64_t)(2 << tpr_log) * rp <= bw * 64) ++tpr_log;
   const int64_t tpr = (int64_t)1 << tpr_log;
   if (tpr < 16) return false;
   const int64_t smn = (KT * (kTileK / 8) + tpr - 1) / tpr;
   if (smn > 32) return false;
   const int64_t vpt = p.M * KT * kTileK / (tpr * rp);
   const int64_t wg_weight_bytes = ngmax * ns * KT * kTileBytes;
-  if (vpt > 128 || (vpt > 64 && wg_weight_bytes <= 64 * 1024)) return false;
+  if (vpt > 128 || (vpt > 96 && wg_weight_bytes <= 64 * 1024)) return false;
   const size_t a_bytes = (size_t)((p.M * stage_stride((int)KT) + 15) / 16) * 16;
   const size_t red = (size_t)(ngmax * w * ns * p.M * 16 * 4);
   if (a_bytes + red > (size_t)kWalkLdsMax) return false;
   wp.grid = (int)G;
   wp.waves = (int)w;
   wp.sets = (int)sets;
+  wp.block_waves = (int)bw;
   wp.tpw = (int)tpw;
   wp.ngroups = (int)ngroups;
   wp.ngmax = (int)ngmax;

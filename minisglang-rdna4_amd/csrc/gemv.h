@@ -636,6 +636,7 @@ struct WalkPlan {
   int grid;
   int waves;    // the plan's K-split waves (one set)
   int sets;     // wave sets per workgroup, each walking every sets-th strip group
+  int block_waves;  // waves per workgroup: the sets, plus helper waves of the row phase
   int tpw;
   int ngroups;
   int ngmax;    // most strip groups of one workgroup

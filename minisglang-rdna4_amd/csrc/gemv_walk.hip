@@ -22,8 +22,8 @@ namespace w4a8 {
 // each thread's chunks as packed 16-bit magnitudes, a 16-lane DPP reduction, then the row's 16-lane
 // groups through LDS. DT: the activation dtype (kBF16 / kF16).
 //
-// Walk: the waves form `sets` sets of kw waves (kw: the plan's K-split waves); set s takes the
-// workgroup's strip groups s, s + sets, ...; wave w of a set owns K tiles [w * tpw, (w + 1) * tpw)
+// Walk: the first sets * kw waves form `sets` sets of kw waves (kw: the plan's K-split waves); set s
+// takes the workgroup's strip groups s, s + sets, ...; wave w of a set owns K tiles [w * tpw, (w + 1) * tpw)
 // of each and keeps CH tiles of weight loads in flight across its groups.
 //   NS: strips per group (plain arm 1; fused silu 2: a gate strip and its up strip).
 template <int NS, int CH, int MODE, bool SYM, int SM, int DT>
@@ -54,8 +54,10 @@ __global__ void __launch_bounds__(512) gemv_walk_kernel(const GemmArgs p, const 
     stg[i] = bload128(rs_x, ok ? (uint32_t)r * ldb + (uint32_t)j * 16u : xbytes, 0u);
   }
 
-  // sets of kw waves (1 or 2): wave w is wave wk of set w >= kw
+  // sets of kw waves (1 or 2): wave w is wave wk of set w >= kw; waves past the sets (a plan of 5-7
+  // waves in an 8-wave workgroup) only help with the row phase
   const int set = (wa.sets == 2 && wave >= kw) ? 1 : 0, wk = wave - set * kw, sets = wa.sets;
+  const bool walker = wave < sets * kw;
   const int N = (int)p.N, KT = (int)p.KT;
   const int nstrips = N / kTileN;
   const int half = p.silu ? NS / 2 : NS;
@@ -70,7 +72,7 @@ __global__ void __launch_bounds__(512) gemv_walk_kernel(const GemmArgs p, const 
   const int kb = wk * tpw;
   const int ke = kb + tpw < KT ? kb + tpw : KT;
   const int nt = ke - kb;  // >= 1: the plan gives every wave at least one tile
-  const int ngs = sets == 2 ? (ng - set + 1) >> 1 : ng;  // this set's groups
+  const int ngs = !walker ? 0 : sets == 2 ? (ng - set + 1) >> 1 : ng;  // this set's groups
   const int nitems = ngs * nt;
   constexpr int kEsz = MODE == kModeE8M0 ? 1 : 2;
   const int ngr = K >> (31 - __builtin_clz((unsigned)p.group));
@@ -301,7 +303,7 @@ void walk_launch_dt(const GemmArgs& p, const WalkPlan& wp, hipStream_t stream) {
       hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, kWalkLdsMax);
   (void)attr;
   const WalkArgs wa{wp.waves, wp.sets, wp.tpw, wp.ngroups / wp.grid, wp.ngroups % wp.grid, wp.tpr_log};
-  hipLaunchKernelGGL(kern, dim3(wp.grid), dim3(wp.waves * wp.sets * 64), wp.lds, stream, p, wa);
+  hipLaunchKernelGGL(kern, dim3(wp.grid), dim3(wp.block_waves * 64), wp.lds, stream, p, wa);
 }
 
 template <int NS, int CH, int MODE, bool SYM, int SM>
