@@ -43,7 +43,7 @@ extern "C" {
 
 /* ABI revision of this header. A client checks w4a8_abi_version() == W4A8_ABI_VERSION at load:
  * revision 3 inserted y_dtype as w4a8_moe_combine's second argument, revision 4 added
- * w4a8_linear_launch_count. */
+ * w4a8_linear_launch_count, w4a8_moe_gelu_tanh_mul and w4a8_moe_gemm2_combine's row_dtype. */
 #define W4A8_ABI_VERSION 4
 int w4a8_abi_version(void);
 
@@ -213,22 +213,35 @@ int w4a8_moe_gemm(const uint8_t* a_fp8, int64_t lda, const float* a_scales, int 
 int w4a8_moe_combine(const void* y, int y_dtype, int64_t ldy, const int32_t* inv_pos, const float* topk_w, int64_t T,
                      int top_k, int64_t H, void* out, int out_dtype, void* stream);
 
+/* Gated tanh-GELU between the unfused gemm1 and gemm2 of the MoE FFN (experts declaring HF
+ * gelu_pytorch_tanh): out[r, i] = gelu_tanh(y[r, i]) * y[r, inter + i] in f32, rounded once to the
+ * dtype of y (bf16/fp16). Replaces the reference's torch gelu_tanh_and_mul that w4a8_moe runs on its
+ * unfused gemm1 output (python/minisgl/layers/activation.py:47-64, python/minisgl/quant/kernels.py:
+ * 777-783). y (rows, ldy >= 2*inter), out (rows, ldo >= inter); row_count: optional device int32
+ * bounding the rows done (the align's ntp). */
+int w4a8_moe_gelu_tanh_mul(const void* y, int dtype, int64_t ldy, int64_t rows, int64_t inter, void* out, int64_t ldo,
+                           const int32_t* row_count, void* stream);
+
 /* Fused gemm2 + top-k weighted combine of the MoE FFN for decode-sized batches: replaces
  * fp8_wmma.mmq_fp8_moe_gemm2_gather_reduce (python/minisgl/quant/kernels.py:831-850), one launch for
  * the per-row act quant of the gemm1 buffer, gemm2 and the combine. a: the gemm1 buffer (P, K)
  * bf16/fp16 at padded positions (row stride lda elements, 16-byte aligned); slot s = t*top_k + j of
  * token t reads row inv_pos[s] (inv_pos < 0: dropped slot) with expert topk_ids[s], quantized per
  * row as w4a8_act_quant does, bit for bit. out (T, N) = sum_j topk_w[t, j] * gemm2(row of slot
- * (t, j)) in f32 over the slots in order, cast to out_dtype: the same bits as w4a8_act_quant +
- * w4a8_moe_gemm (decode arm, block_m, f32 out) + w4a8_moe_combine (f32 y). Deterministic; no
+ * (t, j)) in f32 over the slots in order, cast to out_dtype, each slot's gemm2 row first rounded
+ * to row_dtype (2 = f32: not rounded, as the reference's fused gemm2 + gather-reduce sums them;
+ * 0/1: bf16/fp16, as its unfused gemm2 hands them over): the same bits as w4a8_act_quant +
+ * w4a8_moe_gemm (decode arm, block_m, row_dtype out) + w4a8_moe_combine. Deterministic; no
  * workspace, no atomics.
- * Formats: int4 with groups of 128+, MXFP4 (E8M0) and NVFP4; K % 128 == 0, K <= 2048, top_k <= 16
- * (w4a8_moe_gemm2_combine_supported), else kErrUnsupported (2). */
+ * Formats: int4 with groups of 128+, MXFP4 (E8M0) and NVFP4; K % 128 == 0, K <= 2048, top_k <= 16,
+ * NVFP4 and zero-point int4 with K > 1024 only for top_k <= 8 (w4a8_moe_gemm2_combine_supported),
+ * else kErrUnsupported (2). Revision 4 added row_dtype. */
 int w4a8_moe_gemm2_combine_supported(int64_t K, int scale_fmt, int has_zeros, int wfmt, int64_t group_size, int top_k);
 int w4a8_moe_gemm2_combine(const void* a, int a_dtype, int64_t lda, const int32_t* topk_ids, const float* topk_w,
                            const int32_t* inv_pos, int64_t T, int top_k, int block_m, int64_t P, const void* w_tile,
                            int64_t E, int64_t N, int64_t K, const void* scales, int scale_fmt, const int32_t* zeros,
-                           int wfmt, int64_t group_size, void* out, int out_dtype, int64_t ldo, void* stream);
+                           int wfmt, int64_t group_size, void* out, int out_dtype, int64_t ldo, int row_dtype,
+                           void* stream);
 
 /* ---- W4A16: the same 4-bit weights against unquantized bf16/fp16 activations. */
 

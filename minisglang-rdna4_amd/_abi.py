@@ -56,10 +56,11 @@ SIGNATURES = {
                                _vp, _c_i64, _c_i64, _c_i64, _vp, _c_int, _vp, _c_int, _c_i64,
                                _vp, _c_int, _c_i64, _c_int, _vp, _c_i64, _c_int, _vp]),
     "w4a8_moe_combine": (_c_int, [_vp, _c_int, _c_i64, _vp, _vp, _c_i64, _c_int, _c_i64, _vp, _c_int, _vp]),
+    "w4a8_moe_gelu_tanh_mul": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _c_i64, _vp, _c_i64, _vp, _vp]),
     "w4a8_moe_gemm2_combine_supported": (_c_int, [_c_i64, _c_int, _c_int, _c_int, _c_i64, _c_int]),
     "w4a8_moe_gemm2_combine": (_c_int, [_vp, _c_int, _c_i64, _vp, _vp, _vp, _c_i64, _c_int, _c_int, _c_i64, _vp,
                                         _c_i64, _c_i64, _c_i64, _vp, _c_int, _vp, _c_int, _c_i64, _vp, _c_int,
-                                        _c_i64, _vp]),
+                                        _c_i64, _c_int, _vp]),
     "w4a8_moe_route_gemm1": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _c_int, _c_int, _vp, _c_int, _c_i64, _c_int,
                                       _c_i64, _vp, _c_i64, _c_i64, _vp, _c_int, _vp, _c_int, _c_i64, _vp, _vp, _vp,
                                       _vp, _vp, _vp, _vp, _c_int, _c_i64, _vp]),

@@ -18,7 +18,7 @@ bool gemv_can_fuse_quant(const GemmArgs& p, int64_t row_blocks);
 bool moe_gemm2_combine_fits(int64_t K, int scale_fmt, bool has_zeros, int wfmt, int64_t group, int top_k);
 int launch_moe_gemm2_combine(const GemmArgs& p, int64_t row_blocks, const uint16_t* a, int64_t lda, int adtype,
                              const int32_t* inv_pos, const int32_t* ids, const float* tw, int64_t T, int E,
-                             hipStream_t stream);
+                             int row_dtype, hipStream_t stream);
 size_t gemv_workspace_bytes(int64_t M, int64_t N, int64_t K, int grouped, int64_t row_blocks);
 int launch_prefill(const GemmArgs& p, int64_t rows_to_cover, int bm_rows, hipStream_t stream);
 int launch_prefill_lds(const GemmArgs& p, int64_t rows_to_cover, int bm_rows, hipStream_t stream);
@@ -33,6 +33,8 @@ int launch_moe_route_quant(const void* logits, int ldtype, int64_t T, int E, int
                            int32_t* ids, const void* x, int xdtype, int64_t K, int64_t ldx, uint8_t* xq, int64_t ldq,
                            float* xs, hipStream_t stream);
 int launch_moe_route_gemm1(const GemmArgs& p, int64_t row_blocks, hipStream_t stream);
+int launch_gelu_tanh_mul(const void* y, int64_t ldy, int64_t rows, int64_t inter, int dtype, void* out, int64_t ldo,
+                         const int32_t* row_count, hipStream_t stream);
 int launch_rms_norm(const void* x, int64_t ldx, void* res, int64_t ldr, const void* weight, int plus_one, float eps,
                     int64_t M, int64_t K, int dtype, void* out, int64_t ldo, uint8_t* q, int64_t ldq, float* scales,
                     hipStream_t stream);
@@ -512,6 +514,19 @@ int w4a8_moe_gemm(const uint8_t* a_fp8, int64_t lda, const float* a_scales, int 
   return hip_status(rc, "w4a8_moe_gemm(prefill)");
 }
 
+int w4a8_moe_gelu_tanh_mul(const void* y, int dtype, int64_t ldy, int64_t rows, int64_t inter, void* out, int64_t ldo,
+                           const int32_t* row_count, void* stream) {
+  const char* who = "w4a8_moe_gelu_tanh_mul";
+  if (dtype != kBF16 && dtype != kF16) return fail(kErrInvalid, "%s: y must be bf16 or fp16", who);
+  if (rows < 0 || inter <= 0 || inter % 8)
+    return fail(kErrInvalid, "%s: rows=%lld, inter=%lld (a positive multiple of 8)", who, (long long)rows, (long long)inter);
+  if (ldy < 2 * inter || ldy % 8 || ldo < inter || ldo % 8)
+    return fail(kErrInvalid, "%s: row strides ldy=%lld (>= 2*inter) and ldo=%lld (>= inter), multiples of 8", who,
+                (long long)ldy, (long long)ldo);
+  if (!aligned16(y) || !aligned16(out)) return fail(kErrInvalid, "%s: y and out must be 16-byte aligned", who);
+  return hip_status(launch_gelu_tanh_mul(y, ldy, rows, inter, dtype, out, ldo, row_count, (hipStream_t)stream), who);
+}
+
 int w4a8_moe_gemm2_combine_supported(int64_t K, int scale_fmt, int has_zeros, int wfmt, int64_t group_size, int top_k) {
   return moe_gemm2_combine_fits(K, scale_fmt, has_zeros != 0, wfmt, group_size, top_k) ? 1 : 0;
 }
@@ -519,7 +534,8 @@ int w4a8_moe_gemm2_combine_supported(int64_t K, int scale_fmt, int has_zeros, in
 int w4a8_moe_gemm2_combine(const void* a, int a_dtype, int64_t lda, const int32_t* topk_ids, const float* topk_w,
                            const int32_t* inv_pos, int64_t T, int top_k, int block_m, int64_t P, const void* w_tile,
                            int64_t E, int64_t N, int64_t K, const void* scales, int scale_fmt, const int32_t* zeros,
-                           int wfmt, int64_t group_size, void* out, int out_dtype, int64_t ldo, void* stream) {
+                           int wfmt, int64_t group_size, void* out, int out_dtype, int64_t ldo, int row_dtype,
+                           void* stream) {
   const char* who = "w4a8_moe_gemm2_combine";
   int rc = check_weights(who, N, K, scale_fmt, zeros, wfmt, group_size);
   if (rc) return rc;
@@ -531,6 +547,8 @@ int w4a8_moe_gemm2_combine(const void* a, int a_dtype, int64_t lda, const int32_
     return fail(kErrInvalid, "%s: gemm1 buffer rows must be 16-byte aligned with stride >= K (lda=%lld)", who, (long long)lda);
   if (out_dtype != kBF16 && out_dtype != kF16 && out_dtype != kF32) return fail(kErrInvalid, "%s: unknown output dtype", who);
   if (ldo < N) return fail(kErrInvalid, "%s: ldo=%lld < N=%lld", who, (long long)ldo, (long long)N);
+  if (row_dtype != kBF16 && row_dtype != kF16 && row_dtype != kF32)
+    return fail(kErrInvalid, "%s: unknown row dtype %d", who, row_dtype);
   if (T < 0 || T > 65535 || top_k <= 0) return fail(kErrInvalid, "%s: T=%lld (at most 65535) top_k=%d", who, (long long)T, top_k);
   const int64_t numel = T * top_k;
   if (int rc2 = check_align(who, numel, E, block_m, P)) return rc2;
@@ -552,7 +570,7 @@ int w4a8_moe_gemm2_combine(const void* a, int a_dtype, int64_t lda, const int32_
   p.out = out; p.out_dtype = out_dtype; p.ldo = ldo;
   const int64_t rb = moe_max_blocks(numel, E, block_m, P) * block_m / 16;
   return hip_status(launch_moe_gemm2_combine(p, rb, reinterpret_cast<const uint16_t*>(a), lda, a_dtype, inv_pos,
-                                             topk_ids, topk_w, T, (int)E, (hipStream_t)stream), who);
+                                             topk_ids, topk_w, T, (int)E, row_dtype, (hipStream_t)stream), who);
 }
 
 int w4a8_moe_route_gemm1(const void* logits, int logits_dtype, int64_t T, int64_t E, int top_k, int renormalize,

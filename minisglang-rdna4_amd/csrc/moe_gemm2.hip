@@ -16,9 +16,10 @@
 // Bits: a slot's row sum follows the grouped gemm2's K split (K tiles in runs of tpw, one
 // accumulator per run started from zero, the runs summed in order) with the same per-tile MFMA
 // and FMA sequence, and the combine is the unfused combine's FMA chain, so the output equals the
-// unfused path run with an f32 intermediate (act quant, w4a8_moe_gemm decode arm into f32,
-// w4a8_moe_combine) bit for bit. Like the reference's fused gemm2 + gather-reduce, the slot rows
-// are summed unrounded; its unfused gemm2 hands them over in the activation dtype.
+// unfused path (act quant, w4a8_moe_gemm decode arm into row_dtype, w4a8_moe_combine) bit for bit.
+// row_dtype follows the reference: its fused gemm2 + gather-reduce sums the slot rows unrounded
+// (f32), its unfused gemm2 (NVFP4 two-level weights, or MINISGL_MOE_G2FUSE=0) hands them over in
+// the activation dtype.
 #include "gemv.h"
 
 namespace w4a8 {
@@ -44,16 +45,19 @@ struct G2CArgs {
   void* out;
   int out_dtype;
   int64_t ldo;
+  int row_dtype;          // each slot's gemm2 row rounded to this dtype before the combine (kF32: not)
 };
 
 constexpr int kG2cMaxSlots = 16;
 
 // MODE: kModeI4 (int4, group a multiple of 128), kModeE8M0 (MXFP4), kModeNV (NVFP4). SYM: int4
-// without zero points. KTMAX: most K tiles (weights of every tile are loaded up front).
-template <int MODE, bool SYM, int KTMAX>
-__global__ void __launch_bounds__(kG2cMaxSlots * 64) moe_gemm2_combine_kernel(const G2CArgs p) {
+// without zero points. KTMAX: most K tiles (weights of every tile are loaded up front). SLOTS: most
+// top-k slots (waves) of the launch, 8 or 16: a 16-wave workgroup leaves each wave 128 VGPRs, an
+// 8-wave one 256, which the 16-tile NVFP4 and asymmetric int4 kernels need.
+template <int MODE, bool SYM, int KTMAX, int SLOTS>
+__global__ void __launch_bounds__(SLOTS * 64) moe_gemm2_combine_kernel(const G2CArgs p) {
   extern __shared__ __align__(16) unsigned char arows[];  // per wave: KT*128 fp8 codes + 16 bytes
-  __shared__ float ys[kG2cMaxSlots][kTileN];
+  __shared__ float ys[SLOTS][kTileN];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // top-k slot j
   const int strip = blockIdx.x;
@@ -93,10 +97,14 @@ __global__ void __launch_bounds__(kG2cMaxSlots * 64) moe_gemm2_combine_kernel(co
     const BufRsrc rs_z = make_rsrc(zeros, (MODE == kModeI4 && zeros) ? (uint32_t)(ngroups * (N / 8) * 4) : 0u);
     const int gshift = 31 - __builtin_clz((unsigned)(p.group >= kTileK ? p.group / kTileK : 1));
     uint4 raw[KTMAX];
-    uint16_t sc[KTMAX];
+    // fp16 scales and NVFP4 block-scale bytes land in the 16-bit halves of their registers (a d16
+    // load writes one half without waiting): two scales per VGPR, two NVFP4 bytes per VGPR. Kept
+    // as one value per VGPR, the KTMAX=16 NVFP4 and asymmetric int4 kernels spilled to scratch.
+    typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
+    v2u16 sc[(KTMAX + 1) / 2];
     uint32_t zw[(MODE == kModeI4 && !SYM) ? KTMAX : 1];
     int sb[MODE == kModeE8M0 ? KTMAX : 1];
-    uint8_t nvs[MODE == kModeNV ? KTMAX : 1][8];
+    v2u16 nvs[MODE == kModeNV ? KTMAX : 1][4];
     // every slot up to KTMAX is loaded, those past KT from tile KT-1 again (a cache hit, never
     // used): a guard per tile made the compiler finish each tile's scale before issuing the next
     // tile, one memory round trip per K tile
@@ -106,14 +114,14 @@ __global__ void __launch_bounds__(kG2cMaxSlots * 64) moe_gemm2_combine_kernel(co
       raw[kt] = bload128_nt(rs_w, (uint32_t)lane * 16, (uint32_t)((strip * KT + kc) * kTileBytes));
       if (MODE == kModeI4) {
         const int g = kc >> gshift;
-        sc[kt] = bload16(rs_s, (uint32_t)n * 2, (uint32_t)(g * N * 2));
+        sc[kt >> 1][kt & 1] = bload16(rs_s, (uint32_t)n * 2, (uint32_t)(g * N * 2));
         if (!SYM) zw[(MODE == kModeI4 && !SYM) ? kt : 0] = bload32(rs_z, (uint32_t)(n / 8) * 4, (uint32_t)(g * (N / 8) * 4));
       } else if (MODE == kModeE8M0) {
         sb[MODE == kModeE8M0 ? kt : 0] = (int)bload8(rs_s, (uint32_t)((lane >> 4) * N + n), (uint32_t)(kc * 4 * N));
       } else {
 #pragma unroll
         for (int ss = 0; ss < 8; ++ss)
-          nvs[MODE == kModeNV ? kt : 0][ss] = bload8(rs_s, (uint32_t)n, (uint32_t)((kc * 8 + ss) * N));
+          nvs[MODE == kModeNV ? kt : 0][ss >> 1][ss & 1] = (unsigned short)bload8(rs_s, (uint32_t)n, (uint32_t)((kc * 8 + ss) * N));
       }
     }
 
@@ -157,7 +165,7 @@ __global__ void __launch_bounds__(kG2cMaxSlots * 64) moe_gemm2_combine_kernel(co
         } else if (MODE == kModeI4 && SYM) {
           const v4f seed = mfma_f8f8(at, splat8(0xB0B0B0B0u), zero4);  // -R/2
           const v4f c = mfma_f8f8(at, unpack_tile_int4(raw[kt]), seed);
-          const float scf = f16_to_f32(sc[kt]);
+          const float scf = f16_to_f32(sc[kt >> 1][kt & 1]);
 #pragma unroll
           for (int r = 0; r < 4; ++r) acc[r] = fmaf(scf, c[r], acc[r]);
         } else if (MODE == kModeI4) {
@@ -165,7 +173,7 @@ __global__ void __launch_bounds__(kG2cMaxSlots * 64) moe_gemm2_combine_kernel(co
           const v4f c = mfma_f8f8(at, unpack_tile_int4(raw[kt]), zero4);
           const uint32_t z = zw[(MODE == kModeI4 && !SYM) ? kt : 0];
           const float coef = 15.0f - 2.0f * (float)((z >> (4 * (n & 7))) & 15u);
-          const float scf = f16_to_f32(sc[kt]);
+          const float scf = f16_to_f32(sc[kt >> 1][kt & 1]);
 #pragma unroll
           for (int r = 0; r < 4; ++r) acc[r] = fmaf(scf, fmaf(coef, rh[r], c[r]), acc[r]);
         } else {
@@ -173,7 +181,7 @@ __global__ void __launch_bounds__(kG2cMaxSlots * 64) moe_gemm2_combine_kernel(co
 #pragma unroll
           for (int ss = 0; ss < 8; ++ss) {
             const v4f c = mfma_f8f4_sb(at, fp4_half_operand(b, ss), zero4, subgroup_mask_scale(lane, 8, ss));
-            const float scf = __builtin_amdgcn_cvt_f32_fp8((int)(uint32_t)nvs[MODE == kModeNV ? kt : 0][ss], 0);
+            const float scf = __builtin_amdgcn_cvt_f32_fp8((int)(uint32_t)nvs[MODE == kModeNV ? kt : 0][ss >> 1][ss & 1], 0);
 #pragma unroll
             for (int r = 0; r < 4; ++r) acc[r] = fmaf(scf, c[r], acc[r]);
           }
@@ -190,6 +198,7 @@ __global__ void __launch_bounds__(kG2cMaxSlots * 64) moe_gemm2_combine_kernel(co
     float v = tot[0];
     if (MODE == kModeNV) v *= __int_as_float(zeros[n]);  // the per-output-channel global
     yv = v * s;
+    if (p.row_dtype != kF32) yv = from_dtype(to_dtype(yv, p.row_dtype), p.row_dtype);
   }
   if (lane < kTileN) ys[wave][lane] = yv;
   __syncthreads();
@@ -208,27 +217,34 @@ __global__ void __launch_bounds__(kG2cMaxSlots * 64) moe_gemm2_combine_kernel(co
 }
 
 // True when the fused kernel serves these weights: int4 with groups of 128 or more, MXFP4 (E8M0)
-// or NVFP4, K a multiple of 128 up to 2048, top_k up to 16.
+// or NVFP4, K a multiple of 128 up to 2048, top_k up to 16; NVFP4 and asymmetric int4 past 8 K
+// tiles only for up to 8 slots (their 16-tile kernel does not fit 128 VGPRs).
 bool moe_gemm2_combine_fits(int64_t K, int scale_fmt, bool has_zeros, int wfmt, int64_t group, int top_k) {
-  const bool fmt = (wfmt == kInt4 && scale_fmt == kScaleF16 && group % kTileK == 0) ||
-                   (wfmt == kE2M1 && scale_fmt == kScaleE8M0 && !has_zeros && group == 32) ||
-                   (wfmt == kE2M1 && scale_fmt == kScaleE4M3 && has_zeros && group == 16);
-  return fmt && K % kTileK == 0 && K <= 16 * kTileK && top_k >= 1 && top_k <= kG2cMaxSlots;
+  const bool i4 = wfmt == kInt4 && scale_fmt == kScaleF16 && group % kTileK == 0;
+  const bool nv = wfmt == kE2M1 && scale_fmt == kScaleE4M3 && has_zeros && group == 16;
+  const bool fmt = i4 || nv || (wfmt == kE2M1 && scale_fmt == kScaleE8M0 && !has_zeros && group == 32);
+  const bool wide_ok = !(nv || (i4 && has_zeros)) || K <= 8 * kTileK || top_k <= 8;
+  return fmt && wide_ok && K % kTileK == 0 && K <= 16 * kTileK && top_k >= 1 && top_k <= kG2cMaxSlots;
 }
 
 template <int MODE, bool SYM>
 static void g2c_launch(const G2CArgs& a, dim3 grid, dim3 block, size_t lds, hipStream_t st) {
-  if (a.KT <= 8)
-    hipLaunchKernelGGL((moe_gemm2_combine_kernel<MODE, SYM, 8>), grid, block, lds, st, a);
-  else
-    hipLaunchKernelGGL((moe_gemm2_combine_kernel<MODE, SYM, 16>), grid, block, lds, st, a);
+  const bool few = a.top_k <= 8;
+  if (a.KT <= 8 && few)
+    hipLaunchKernelGGL((moe_gemm2_combine_kernel<MODE, SYM, 8, 8>), grid, block, lds, st, a);
+  else if (a.KT <= 8)
+    hipLaunchKernelGGL((moe_gemm2_combine_kernel<MODE, SYM, 8, 16>), grid, block, lds, st, a);
+  else if (few)
+    hipLaunchKernelGGL((moe_gemm2_combine_kernel<MODE, SYM, 16, 8>), grid, block, lds, st, a);
+  else if constexpr (MODE != kModeNV && (MODE != kModeI4 || SYM))
+    hipLaunchKernelGGL((moe_gemm2_combine_kernel<MODE, SYM, 16, 16>), grid, block, lds, st, a);
 }
 
 // p: the grouped gemm2's arguments as w4a8_moe_gemm would build them for the decode arm (for the
 // K split); the rest is the fused kernel's. The caller checked moe_gemm2_combine_fits.
 int launch_moe_gemm2_combine(const GemmArgs& p, int64_t row_blocks, const uint16_t* a, int64_t lda, int adtype,
                              const int32_t* inv_pos, const int32_t* ids, const float* tw, int64_t T, int E,
-                             hipStream_t stream) {
+                             int row_dtype, hipStream_t stream) {
   int waves = 0, tpw = 0;
   gemv_ksplit(p, row_blocks, waves, tpw);
   G2CArgs g = {};
@@ -238,7 +254,7 @@ int launch_moe_gemm2_combine(const GemmArgs& p, int64_t row_blocks, const uint16
   g.scales = p.scales; g.s_expert_stride = p.s_expert_stride;
   g.zeros = p.zeros; g.z_expert_stride = p.z_expert_stride;
   g.group = p.group; g.N = (int)p.N; g.K = (int)p.K; g.KT = (int)p.KT; g.tpw = tpw;
-  g.out = p.out; g.out_dtype = p.out_dtype; g.ldo = p.ldo;
+  g.out = p.out; g.out_dtype = p.out_dtype; g.ldo = p.ldo; g.row_dtype = row_dtype;
   const dim3 grid((unsigned)(p.N / kTileN), (unsigned)T);
   const dim3 block((unsigned)(p.top_k * 64));
   const size_t lds = (size_t)p.top_k * (p.KT * kTileK + 16);

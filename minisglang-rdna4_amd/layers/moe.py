@@ -224,12 +224,22 @@ class MoEQuantMethod:
         raise NotImplementedError(f"{type(self).__name__} does not support expert parallelism")
 
 
-_W4A8_ACTIVATIONS = ("silu",)
+# gated activations the w4a8_moe family serves (python/minisgl/layers/moe.py:583-587): "gelu" is HF
+# gelu_pytorch_tanh (Gemma4's routed experts), on the unfused gemm1 + gated tanh-GELU path
+_W4A8_ACTIVATIONS = ("silu", "gelu")
 
 
 def _check_activation(scheme: str, activation: str, allowed=_W4A8_ACTIVATIONS) -> None:
     if activation not in allowed:
         raise NotImplementedError(f"MoE {scheme} path supports activation {'|'.join(allowed)}; got {activation!r}")
+
+
+def _reject_w4a16_activation(activation: str) -> None:
+    # the W4A16 expert arm's tail is silu only: a gelu model reaching it would get well-formed wrong
+    # numbers, so it is refused loudly (python/minisgl/layers/moe.py:678-690)
+    if activation != "silu":
+        raise NotImplementedError(f"MoE W4A16 (MINISGL_MOE_W4A16=1) is silu-only; got activation {activation!r}. "
+                                  "Unset MINISGL_MOE_W4A16 to serve this model through the W4A8 path.")
 
 
 class _W4A8MoEMethod(MoEQuantMethod):
@@ -258,6 +268,7 @@ class _W4A8MoEMethod(MoEQuantMethod):
         _check_activation("W4A8", activation)
         assert not apply_router_weight_on_input, "MoE W4A8 path has no router-weight-on-input"
         if _moe_w4a16():
+            _reject_w4a16_activation(activation)
             # fp16 activations, never quantized: a producer's fp8 pair has nothing to feed and is dropped
             return _w4a16_experts(self._quant, w13, w2, hidden_states, topk_weights, topk_ids, router_logits, top_k,
                                   renormalize, False)
@@ -269,6 +280,7 @@ class _W4A8MoEMethod(MoEQuantMethod):
     def ep_local(self, w13, w2, g_hidden, local_weights, local_ids, *, top_k, renormalize, activation="silu"):
         _check_activation("W4A8", activation)
         if _moe_w4a16():
+            _reject_w4a16_activation(activation)
             return _w4a16_experts(self._quant, w13, w2, g_hidden, local_weights, local_ids, None, top_k, renormalize,
                                   False)
         return kernels.w4a8_moe(g_hidden, w13._w_op, w13._scales_op, w13._zeros_op,
@@ -294,6 +306,7 @@ class _MxFp4MoEMethod(MoEQuantMethod):
         _check_activation("MXFP4", activation)
         assert not apply_router_weight_on_input, "MoE MXFP4 path has no router-weight-on-input"
         if _moe_w4a16():
+            _reject_w4a16_activation(activation)
             return _w4a16_experts(self._quant, w13, w2, hidden_states, topk_weights, topk_ids, router_logits, top_k,
                                   renormalize, True)
         return kernels.w4a8_moe(hidden_states, w13._w_op, w13._scales_op, None, w2._w_op, w2._scales_op, None,
@@ -303,6 +316,7 @@ class _MxFp4MoEMethod(MoEQuantMethod):
     def ep_local(self, w13, w2, g_hidden, local_weights, local_ids, *, top_k, renormalize, activation="silu"):
         _check_activation("MXFP4", activation)
         if _moe_w4a16():
+            _reject_w4a16_activation(activation)
             return _w4a16_experts(self._quant, w13, w2, g_hidden, local_weights, local_ids, None, top_k, renormalize,
                                   True)
         return kernels.w4a8_moe(g_hidden, w13._w_op, w13._scales_op, None, w2._w_op, w2._scales_op, None,
@@ -330,6 +344,7 @@ class _NvFp4MoEMethod(MoEQuantMethod):
         _check_activation("NVFP4", activation)
         assert not apply_router_weight_on_input, "MoE NVFP4 path has no router-weight-on-input"
         if _moe_w4a16() and hidden_states.shape[0] <= _NVFP4_A16_DECODE_MAX:
+            _reject_w4a16_activation(activation)
             return kernels.w4a16_moe_decode(hidden_states, *self.plane(w13), *self.plane(w2), hidden_states.shape[1],
                                             topk_weights=topk_weights, topk_ids=topk_ids, router_logits=router_logits,
                                             top_k=top_k, renormalize=renormalize)

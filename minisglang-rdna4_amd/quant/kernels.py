@@ -671,15 +671,17 @@ def _check_moe_scale_pair(w: torch.Tensor, scales: torch.Tensor, zeros: "torch.T
 
 
 def _moe_gemm2_combine(buf2, topk_ids, tw, inv, T, top_k, bm, P, tiles, E, H, inter, scales, sfmt, zeros, wfmt,
-                       group, out):
+                       group, out, row_dtype):
     """gemm2 (per-row requant of the gemm1 buffer in the prologue) + top-k weighted combine as one
-    launch: fp8_wmma.mmq_fp8_moe_gemm2_gather_reduce (python/minisgl/quant/kernels.py:831-850)."""
+    launch: fp8_wmma.mmq_fp8_moe_gemm2_gather_reduce (python/minisgl/quant/kernels.py:831-850);
+    each slot's gemm2 row rounded to row_dtype first (float32: not rounded)."""
     lib = _abi.load()
     _abi.check(
         lib.w4a8_moe_gemm2_combine(_abi.ptr(buf2), _abi.dtype_code(buf2.dtype), buf2.stride(0), _abi.ptr(topk_ids),
                                    _abi.ptr(tw), _abi.ptr(inv), T, top_k, bm, P, _abi.ptr(tiles), E, H, inter,
                                    _abi.ptr(scales), sfmt, _abi.ptr(zeros), wfmt, group, _abi.ptr(out),
-                                   _abi.dtype_code(out.dtype), out.stride(0), _abi.stream_of(buf2)),
+                                   _abi.dtype_code(out.dtype), out.stride(0), _abi.dtype_code(row_dtype),
+                                   _abi.stream_of(buf2)),
         "w4a8_moe gemm2+combine",
     )
 
@@ -734,10 +736,13 @@ def _moe_forward(x, w13, w13_scales, w13_zeros, w2, w2_scales, w2_zeros, gating_
                  topk_weights=None, topk_ids=None, block_m=None, weight_is_e2m1=False, activation="silu",
                  x_fp8=None, act_scales=None, y2_dtype=None) -> dict:
     """w4a8_moe's pipeline; returns the output and every intermediate (route, align, the (P, inter)
-    gemm1 buffer) so each stage can be checked on its own. y2_dtype: dtype of the unfused gemm2's
-    (P, K) rows handed to the combine: x's dtype by default, as the reference's unfused gemm2 returns
-    them (tools/vhip_patches/moe_experts.py:874-880, python/minisgl/quant/kernels.py:866-882);
-    torch.float32 keeps them unrounded, which is what the fused gemm2 + combine sums."""
+    gemm1 buffer) so each stage can be checked on its own. The gemm2 rows reach the combine as the
+    reference hands them over: unrounded (f32) where it runs its fused decode gemm2 + gather-reduce
+    (MINISGL_MOE_G2FUSE on, no NVFP4 two-level scales, M <= 32, block_m != 128:
+    python/minisgl/quant/kernels.py:836-850), in x's dtype where it runs the unfused gemm2
+    (kernels.py:852-882, tools/vhip_patches/moe_experts.py:874-880); this holds on both of this
+    build's gemm2 paths ("round_y2" in the result). y2_dtype overrides the unfused path's row dtype
+    (tests run it in f32 to compare with the fused kernel)."""
     M, K = x.shape
     E = w13.shape[0]
     _grp = (K // w13_scales.shape[1]) if w13_scales.dim() == 3 else -1
@@ -749,8 +754,6 @@ def _moe_forward(x, w13, w13_scales, w13_zeros, w2, w2_scales, w2_zeros, gating_
     _check_moe_scale_pair(w2, w2_scales, w2_zeros, "w2")
     assert activation in ("silu", "gelu"), (
         f"w4a8_moe supports activation 'silu' or 'gelu' (gelu_pytorch_tanh); got {activation!r}")
-    if activation != "silu":
-        raise NotImplementedError("w4a8_moe: only the fused silu epilogue is built for MI355X")
     if x.dtype not in (torch.bfloat16, torch.float16):
         raise TypeError(f"w4a8_moe: x must be bf16/fp16, got {x.dtype}")
     N1 = _n_of(w13)
@@ -792,7 +795,9 @@ def _moe_forward(x, w13, w13_scales, w13_zeros, w2, w2_scales, w2_zeros, gating_
     # T=16 68.8 -> 79.0, so the align stays from there on
     slots = M <= _MOE_SLOTS_MAX and block_m < 64
     buf2 = None
-    if topk_ids is None and x_fp8 is None and slots and _MOE_ROUTED:
+    gelu = activation == "gelu"
+    buf1 = None
+    if topk_ids is None and x_fp8 is None and slots and _MOE_ROUTED and not gelu:
         # route, slots, the per-token quant of x and gemm1 in one launch (same bits as below)
         r = _route_gemm1(gating_output, top_k, renormalize, E, block_m, x, t13, N1, w13s, s13f, w13z, wfmt, _grp)
         if r is not None:
@@ -818,15 +823,33 @@ def _moe_forward(x, w13, w13_scales, w13_zeros, w2, w2_scales, w2_zeros, gating_
             xq, xs = act_quant(x)
         P = sorted_ids.shape[0]
         buf2 = torch.empty((P, inter), dtype=x.dtype, device=x.device)
-        engaged(f"w4a8_mi355x.moe_gemm1_silu({arm_name}{e2}{'+prequant' if x_fp8 is not None else ''})")
-        _moe_gemm(xq, K, xs, 1, sorted_ids, expert_ids, ntp, topk_ids.numel(), top_k, block_m, P, t13, E, N1, K,
-                  w13s, s13f, w13z, wfmt, _grp, buf2, _abi.dtype_code(x.dtype), inter, True, arm, "w4a8_moe gemm1")
+        pq = '+prequant' if x_fp8 is not None else ''
+        if gelu:
+            # HF gelu_pytorch_tanh experts: the unfused gemm1 ((P, 2*inter) in x's dtype), then the
+            # gated tanh-GELU (python/minisgl/quant/kernels.py:768-783)
+            buf1 = torch.empty((P, N1), dtype=x.dtype, device=x.device)
+            engaged(f"w4a8_mi355x.moe_gemm1({arm_name}{e2}{pq})")
+            _moe_gemm(xq, K, xs, 1, sorted_ids, expert_ids, ntp, topk_ids.numel(), top_k, block_m, P, t13, E, N1, K,
+                      w13s, s13f, w13z, wfmt, _grp, buf1, _abi.dtype_code(x.dtype), N1, False, arm, "w4a8_moe gemm1")
+            engaged("w4a8_mi355x.moe_gelu_tanh_mul")
+            _abi.check(_abi.load().w4a8_moe_gelu_tanh_mul(_abi.ptr(buf1), _abi.dtype_code(x.dtype), N1, P, inter,
+                                                          _abi.ptr(buf2), inter, _abi.ptr(ntp), _abi.stream_of(x)),
+                       "w4a8_moe gelu_tanh_mul")
+        else:
+            engaged(f"w4a8_mi355x.moe_gemm1_silu({arm_name}{e2}{pq})")
+            _moe_gemm(xq, K, xs, 1, sorted_ids, expert_ids, ntp, topk_ids.numel(), top_k, block_m, P, t13, E, N1, K,
+                      w13s, s13f, w13z, wfmt, _grp, buf2, _abi.dtype_code(x.dtype), inter, True, arm, "w4a8_moe gemm1")
     P = sorted_ids.shape[0]
     numel = topk_ids.numel()
 
     lib = _abi.load()
     w2s = w2_scales.contiguous()
     w2z = w2_zeros.contiguous() if w2_zeros is not None else None
+    # the reference's choice between its fused decode gemm2 + gather-reduce (rows summed unrounded)
+    # and its unfused gemm2 (rows in x's dtype), kernels.py:836
+    round_y2 = not (_MOE_G2FUSE and s2f != _abi.SCALE_E4M3 and s13f != _abi.SCALE_E4M3
+                    and M <= _MOE_GEMM1_GEMV_MAX and block_m != 128)
+    row_dt = x.dtype if round_y2 else torch.float32
     fuse2 = (_MOE_G2FUSE and arm == _abi.KERNEL_DECODE and M <= _MOE_G2C_MAX_TOKENS
              and lib.w4a8_moe_gemm2_combine_supported(inter, s2f, int(w2_zeros is not None), wfmt, _grp2, top_k) == 1)
     if fuse2:
@@ -834,10 +857,10 @@ def _moe_forward(x, w13, w13_scales, w13_zeros, w2, w2_scales, w2_zeros, gating_
         out = torch.empty((M, K), dtype=x.dtype, device=x.device)
         engaged(f"w4a8_mi355x.moe_gemm2_combine({arm_name}{e2})")
         _moe_gemm2_combine(buf2, topk_ids, topk_weights, inv, M, top_k, block_m, P, t2, E, K, inter, w2s, s2f, w2z,
-                           wfmt, _grp2, out)
-        return {"out": out, "buf2": buf2, "y2": None, "topk_weights": topk_weights, "topk_ids": topk_ids,
+                           wfmt, _grp2, out, row_dt)
+        return {"out": out, "buf1": buf1, "buf2": buf2, "y2": None, "topk_weights": topk_weights, "topk_ids": topk_ids,
                 "sorted_ids": sorted_ids, "expert_ids": expert_ids, "ntp": ntp, "inv_pos": inv, "block_m": block_m,
-                "fused_gemm2": True}
+                "fused_gemm2": True, "round_y2": round_y2}
 
     # gemm2 input: per-row fp8 re-quant of the (P, inter) buffer, rows bounded by ntp on device
     q2 = torch.empty((P, inter), dtype=torch.uint8, device=x.device)
@@ -847,9 +870,9 @@ def _moe_forward(x, w13, w13_scales, w13_zeros, w2, w2_scales, w2_zeros, gating_
     rows = min(P, (numel // block_m + min(E, numel)) * block_m)
     _abi.check(lib.w4a8_act_quant(_abi.ptr(buf2), _abi.dtype_code(x.dtype), rows, inter, inter, _abi.ptr(q2), inter,
                                   _abi.ptr(s2), _abi.ptr(ntp), _abi.stream_of(x)), "w4a8_moe act_quant(gemm2)")
-    # gemm2's (P, K) rows in x's dtype, as the reference's unfused gemm2 returns them; the combine
-    # sums them in f32
-    ydt = x.dtype if y2_dtype is None else y2_dtype
+    # gemm2's (P, K) rows in the dtype the reference hands them over in (above); the combine sums
+    # them in f32
+    ydt = row_dt if y2_dtype is None else y2_dtype
     y2 = torch.empty((P, K), dtype=ydt, device=x.device)
     engaged(f"w4a8_mi355x.moe_gemm2({arm_name}{e2})")
     _moe_gemm(q2, inter, s2, 0, sorted_ids, expert_ids, ntp, numel, top_k, block_m, P, t2, E, K, inter,
@@ -859,9 +882,9 @@ def _moe_forward(x, w13, w13_scales, w13_zeros, w2, w2_scales, w2_zeros, gating_
     _abi.check(lib.w4a8_moe_combine(_abi.ptr(y2), _abi.dtype_code(ydt), K, _abi.ptr(inv), _abi.ptr(topk_weights), M,
                                     top_k, K, _abi.ptr(out), _abi.dtype_code(x.dtype), _abi.stream_of(x)),
                "w4a8_moe combine")
-    return {"out": out, "buf2": buf2, "y2": y2, "topk_weights": topk_weights, "topk_ids": topk_ids,
+    return {"out": out, "buf1": buf1, "buf2": buf2, "y2": y2, "topk_weights": topk_weights, "topk_ids": topk_ids,
             "sorted_ids": sorted_ids, "expert_ids": expert_ids, "ntp": ntp, "inv_pos": inv, "block_m": block_m,
-            "fused_gemm2": False}
+            "fused_gemm2": False, "round_y2": ydt != torch.float32}
 
 
 def _w4a16_moe_forward(x, w13, w13_scales, w13_zeros, w2, w2_scales, w2_zeros, *, dt, topk_weights=None,

@@ -147,5 +147,5 @@ def test_nvfp4_moe(kernels, oracle, dev, T, bm):
     sorted_ids, expert_ids, ntp, _ = oracle.moe_align(ids, e, 16)
     ref = oracle.moe_forward(synth.bits16(x[sub]), 0, tw, sorted_ids, expert_ids, ntp, 16, top_k, w13.numpy(),
                              s13.view(torch.uint8).numpy(), g13.numpy(), w2.numpy(), s2.view(torch.uint8).numpy(),
-                             g2.numpy(), e2m1=True, nvfp4=True, round_y2=not res["fused_gemm2"])
+                             g2.numpy(), e2m1=True, nvfp4=True, round_y2=res["round_y2"])
     _assert_end_to_end(out[sub.to(dev)], ref, y2ref, rel2, f"nvfp4 moe T={T} bm={bm}")

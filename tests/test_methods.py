@@ -202,8 +202,14 @@ def test_moe_method_selection_and_containers():
     for q in (None, FP8):
         with pytest.raises(NotImplementedError):
             L_.create_moe_quant_method(q)
+    # silu and gelu (HF gelu_pytorch_tanh) are served; anything else is refused by name, and the
+    # silu-only W4A16 arm refuses gelu (python/minisgl/layers/moe.py:583-593, 678-690)
+    L_._check_activation("W4A8", "gelu")
     with pytest.raises(NotImplementedError, match="activation"):
-        L_._check_activation("W4A8", "gelu")
+        L_._check_activation("W4A8", "gelu_erf")
+    with pytest.raises(NotImplementedError, match="silu-only"):
+        L_._reject_w4a16_activation("gelu")
+    L_._reject_w4a16_activation("silu")
 
 
 def test_moe_containers_post_load_per_expert():
