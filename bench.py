@@ -28,7 +28,8 @@ producer_norm_step times the same sweep with its inputs coming out of the RMSNor
 producer: once with the linear quantizing its bf16 input, once with the producer's fp8 pair
 (no act-quant launches).
 
-Modes for profiling runs (same committed file): --profile-kernel runs only the roofline loop,
+Modes for profiling runs (same committed file): --read-floor times the streaming-read floor of one
+launch at the decode weight sizes, --profile-kernel runs only the roofline loop,
 --profile-prefill FMT M K N times one prefill GEMM, --copy-calib runs a plain device copy of known
 size (for scaling rocprofv3 byte counters).
 """
@@ -249,6 +250,55 @@ def _time_calls(calls, reps: int) -> float:
     return a.elapsed_time(b) * 1e3 / reps
 
 
+def read_floor(dev) -> dict:
+    """The HBM streaming-read floor of one launch (w4a8_probe_read): for each decode call's weight
+    size, the fastest of 17 launch shapes of a plain read kernel (one-shot grids of U 16-byte loads per
+    thread and T threads per workgroup, persistent grids of G workgroups), 60 back-to-back launches
+    over 10 buffer copies (more than the 256 MB MALL) bracketed by one event pair on the launching
+    stream, as the decode GEMV's per-call times are taken; plus an empty launch (one 64-thread
+    workgroup reading 16 bytes) timed the same way."""
+    import torch
+
+    lib = importlib.import_module("minisglang-rdna4_amd._abi").load()
+    sizes = {"o_proj M=1 (4096x4096)": 8667136, "qkv M=1 (4096x6144)": 12996608,
+             "down M=1 (14336x4096)": 30314496, "gate_up M=1 (4096x28672)": 60620800,
+             "MXFP4 M=1 (8192x28672)": 124854272}
+    shapes = [(4, 256, 0), (8, 256, 0), (16, 256, 0), (4, 512, 0), (8, 512, 0), (8, 1024, 0), (4, 256, 1024),
+              (8, 256, 1024), (8, 512, 512), (8, 512, 1024), (4, 1024, 256), (8, 1024, 256), (4, 1024, 512),
+              (8, 256, 2048), (16, 256, 1024), (8, 512, 768), (4, 512, 2048)]
+    maxb = max(sizes.values())
+    bufs = [torch.full((maxb,), i + 1, dtype=torch.uint8, device=dev) for i in range(10)]
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream()
+    sptr = stream.cuda_stream
+
+    def timed(launch, reps=60):
+        for i in range(10):
+            launch(bufs[i % 10])
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for i in range(reps):
+            launch(bufs[i % 10])
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) * 1e3 / reps
+
+    out = {}
+    for name, nb in sizes.items():
+        best = None
+        for u, t, g in shapes:
+            us = timed(lambda buf: lib.w4a8_probe_read(buf.data_ptr(), nb, u, t, g, sink.data_ptr(), sptr))
+            if best is None or us < best[0]:
+                best = (us, f"{'persist' if g else 'oneshot'} U={u} T={t}" + (f" G={g}" if g else ""))
+        gbs = nb / (best[0] * 1e-6) / 1e9
+        out[name] = {"bytes": nb, "shape": best[1], "us": round(best[0], 2), "GB/s": round(gbs, 1),
+                     "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+    out["empty launch"] = {"us": round(timed(lambda buf: lib.w4a8_probe_read(buf.data_ptr(), 16, 1, 64, 1,
+                                                                             sink.data_ptr(), sptr)), 2)}
+    return out
+
+
 def _rand_words(shape, gen, dev):
     import torch
 
@@ -458,6 +508,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--profile-kernel", action="store_true")
     ap.add_argument("--copy-calib", action="store_true")
+    ap.add_argument("--read-floor", action="store_true",
+                    help="time the streaming-read floor of one launch at the decode weight sizes and exit")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-configs", action="store_true")
@@ -488,6 +540,9 @@ def main() -> int:
             b.copy_(a)
         torch.cuda.synchronize()
         print(json.dumps({"copy_calib_bytes_read": n, "copy_calib_bytes_written": n}))
+        return 0
+    if args.read_floor:
+        print(json.dumps({"read_floor": read_floor(dev)}))
         return 0
     if args.profile_kernel:
         r = roofline_leg(kernels, dev)

@@ -1,4 +1,5 @@
-"""ctypes binding of libw4a8_mi355x.so (declarations: include/w4a8_mi355x.h).
+"""ctypes binding of libw4a8_mi355x.so (declarations: include/w4a8_mi355x.h and the measurement probe
+of include/w4a8_probe.h).
 
 The library is the only compute path: if it is missing, or no GPU is present, calls raise. There
 is no CPU fallback.
@@ -37,6 +38,8 @@ SIGNATURES = {
     "w4a8_linear_workspace_bytes": (_c_i64, [_c_i64, _c_i64]),
     "w4a8_linear": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _c_i64, _vp, _c_i64, _vp, _c_int, _vp, _c_int, _c_i64,
                              _vp, _c_int, _c_i64, _c_int, _vp, _c_i64, _c_int, _vp]),
+    # measurement probe (include/w4a8_probe.h), not part of the W4A8 path
+    "w4a8_probe_read": (_c_int, [_vp, _c_i64, _c_int, _c_int, _c_int, _vp, _vp]),
     "w4a8_linear_launch_count": (_c_int, [_c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_i64, _c_int,
                                           _c_int]),
     "w4a8_linear_noalloc_max_bytes": (_c_i64, []),

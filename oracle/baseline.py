@@ -29,10 +29,22 @@ def _dequant_int4(w_packed: torch.Tensor, scales: torch.Tensor, group: int) -> t
 
 
 def cpu_model() -> str:
-    """The host CPU's model name (lscpu's 'Model name', read from /proc/cpuinfo)."""
+    """The host CPU as lscpu reports it: 'Model name', with the family / model / stepping numbers
+    and the socket count (a virtualized host may report only a family name such as "AMD EPYC");
+    /proc/cpuinfo's model name if lscpu is missing."""
+    import subprocess
+
     try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        f = {k.strip(): v.strip() for k, v in (ln.split(":", 1) for ln in out.splitlines() if ":" in ln)}
+        if f.get("Model name"):
+            extra = ", ".join(f"{k.lower()} {f[k]}" for k in ("CPU family", "Model", "Stepping", "Socket(s)") if k in f)
+            return f"{f['Model name']} ({extra})" if extra else f["Model name"]
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
                 if line.startswith("model name"):
                     return line.split(":", 1)[1].strip()
     except OSError:
