@@ -25,10 +25,10 @@ namespace w4a8 {
 // K split of a grid of `groups` workgroups: up to 8 waves owning at least 4 K tiles each; grids
 // that would pass ~8192 waves get fewer, longer waves; grids of under ~2 waves per SIMD (the MoE
 // decode calls over a handful of experts, narrow dense weights) halve the tiles per wave, down to
-// 2 and up to 8 waves, so more of the weight bytes are in flight at once.
-static void plan_ksplit(int64_t KT, int64_t groups, int64_t& waves, int64_t& tpw) {
+// 2 and up to 8 waves, so more of the weight bytes are in flight at once. wmax caps the waves.
+static void plan_ksplit(int64_t KT, int64_t groups, int64_t wmax, int64_t& waves, int64_t& tpw) {
   int64_t w = (KT + 3) / 4;
-  if (w > 8) w = 8;
+  if (w > wmax) w = wmax;
   if (w < 1) w = 1;
   // a power of two: 4 waves (two walking sets) rather than 5-7 (K=2560 N=9728 M=16 12.7 -> 10.5 us,
   // M=1 8.5 -> 7.5; K=2816 N=4096 M=1 6.2 -> 5.4 on gemv_kernel)
@@ -47,6 +47,15 @@ static void plan_ksplit(int64_t KT, int64_t groups, int64_t& waves, int64_t& tpw
   tpw = t;
 }
 
+// Wave cap of a call's K split, from (N, K, format) alone. Dense NVFP4 on wide weights (1024+
+// strips) splits K over at most 4 waves of longer ranges: the 8 scaled MFMAs and 8 scale-byte loads
+// of every NVFP4 tile make short waves pay their prologue and reduction more often than the extra
+// loads in flight return. K=8192 N=28672, 8 -> 4 waves: M=1 42.6 -> 37.2 us, M=2 40.2 -> 36.2,
+// M=16 57.7 -> 46.1; on K=28672 N=8192 (512 strips) 4 waves lose (M=1 38.7 -> 41.5), so it keeps 8.
+static int64_t ksplit_wmax(const GemmArgs& p, int64_t strips) {
+  return gemv_nvfp4(p) && !p.sorted_ids && strips >= 1024 ? 4 : 8;
+}
+
 GemvPlan plan_gemv(const GemmArgs& p, int64_t row_blocks, bool quant_src) {
   GemvPlan pl;
   const int64_t KT = (p.K + kTileK - 1) / kTileK;
@@ -62,7 +71,7 @@ GemvPlan plan_gemv(const GemmArgs& p, int64_t row_blocks, bool quant_src) {
   // dense: the one-row grid (one strip per workgroup, one row block); grouped: the launched grid
   const int64_t split_groups = p.sorted_ids ? (strips + pl.nstr - 1) / pl.nstr * row_blocks : strips;
   int64_t w, tpw;
-  plan_ksplit(KT, split_groups, w, tpw);
+  plan_ksplit(KT, split_groups, ksplit_wmax(p, strips), w, tpw);
   pl.waves = (int)w;
   pl.tpw = (int)tpw;
 
@@ -127,11 +136,16 @@ bool plan_gemv_walk(const GemmArgs& p, int64_t row_blocks, WalkPlan& wp) {
   if (p.sorted_ids || row_blocks != 1 || p.M < 1 || p.M > 16 || !p.xsrc) return false;
   const bool i4 = p.wfmt == kInt4 && p.group % kTileK == 0;
   const bool e8 = p.wfmt == kE2M1 && p.sfmt == kScaleE8M0;
-  if (!i4 && !e8) return false;
+  const bool nv = gemv_nvfp4(p);
+  if (!i4 && !e8 && !nv) return false;
   const int64_t KT = p.KT, strips = p.N / kTileN;
   if (e8 && p.M == 1 && strips >= 1024) return false;
+  // NVFP4 (8 MFMAs and 8 scale-byte loads per tile) walks only where the other path reads A per tile
+  // (more than 4 rows): K=8192 N=28672 M=8 48.0 against 52.3 us, but M=4 45.5 against 43.2, M=1 43.2
+  // against 39.3
+  if (nv && p.M <= 4) return false;
   int64_t w, tpw;
-  plan_ksplit(KT, strips, w, tpw);  // the one-row plan: the output bits of gemv_kernel's one-row call
+  plan_ksplit(KT, strips, ksplit_wmax(p, strips), w, tpw);  // the one-row plan: the output bits of gemv_kernel's one-row call
   const int ns = p.silu ? 2 : 1;
   const int64_t ngroups = p.silu ? strips / 2 : strips;
   int64_t rp = 1;
@@ -148,7 +162,7 @@ bool plan_gemv_walk(const GemmArgs& p, int64_t row_blocks, WalkPlan& wp) {
   const int64_t tpr = (int64_t)1 << tpr_log;
   if (tpr < 16) return false;
   const int64_t smn = (KT * (kTileK / 8) + tpr - 1) / tpr;
-  if (smn > 32) return false;
+  if (smn > 16) return false;  // 32 row loads per thread spill (and only odd row counts reach them)
   const int64_t vpt = p.M * KT * kTileK / (tpr * rp);
   const int64_t wg_weight_bytes = ngmax * ns * KT * kTileBytes;
   if (vpt > 128 || (vpt > 96 && wg_weight_bytes <= 64 * 1024)) return false;
@@ -163,7 +177,7 @@ bool plan_gemv_walk(const GemmArgs& p, int64_t row_blocks, WalkPlan& wp) {
   wp.ngroups = (int)ngroups;
   wp.ngmax = (int)ngmax;
   wp.tpr_log = tpr_log;
-  wp.sm = smn <= 1 ? 1 : smn <= 2 ? 2 : smn <= 4 ? 4 : smn <= 8 ? 8 : smn <= 16 ? 16 : 32;
+  wp.sm = smn <= 1 ? 1 : smn <= 2 ? 2 : smn <= 4 ? 4 : smn <= 8 ? 8 : 16;
   wp.lds = a_bytes + red;
   return true;
 }

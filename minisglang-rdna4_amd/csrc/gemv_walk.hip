@@ -28,7 +28,7 @@ namespace w4a8 {
 //   NS: strips per group (plain arm 1; fused silu 2: a gate strip and its up strip).
 template <int NS, int CH, int MODE, bool SYM, int SM, int DT>
 __global__ void __launch_bounds__(512) gemv_walk_kernel(const GemmArgs p, const WalkArgs wa) {
-  static_assert(MODE == kModeI4 || MODE == kModeE8M0, "int4 (groups of 128+) and MXFP4");
+  static_assert(MODE == kModeI4 || MODE == kModeE8M0 || MODE == kModeNV, "int4 (groups of 128+), MXFP4, NVFP4");
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ float amax16[32];  // maxima of the 16-lane groups (8 waves x 4)
   __shared__ float srow[16];
@@ -74,7 +74,7 @@ __global__ void __launch_bounds__(512) gemv_walk_kernel(const GemmArgs p, const 
   const int nt = ke - kb;  // >= 1: the plan gives every wave at least one tile
   const int ngs = !walker ? 0 : sets == 2 ? (ng - set + 1) >> 1 : ng;  // this set's groups
   const int nitems = ngs * nt;
-  constexpr int kEsz = MODE == kModeE8M0 ? 1 : 2;
+  constexpr int kEsz = MODE == kModeI4 ? 2 : 1;
   const int ngr = K >> (31 - __builtin_clz((unsigned)p.group));
   const int gshift = 31 - __builtin_clz((unsigned)(p.group >= kTileK ? p.group / kTileK : 1));
   const BufRsrc rs_w = make_rsrc(p.wt, (uint32_t)(nstrips * KT * kTileBytes));
@@ -85,6 +85,9 @@ __global__ void __launch_bounds__(512) gemv_walk_kernel(const GemmArgs p, const 
   v2h sc[(CH + 1) / 2][NS];
   uint32_t zw[SYM ? 1 : CH][NS];
   int sb[MODE == kModeE8M0 ? CH : 1][NS];
+  // NVFP4: the 8 group-16 scale bytes of a tile, two per register (d16 loads into the halves)
+  typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
+  v2u16 nvs[MODE == kModeNV ? CH : 1][NS][4];
   // item (g, t): K tile kb + t of strip group g0 + g; past the last item the last one is loaded
   // again (a cache hit that keeps the loads unconditional)
   auto load_item = [&](int s, int g, int t) {
@@ -106,8 +109,14 @@ __global__ void __launch_bounds__(512) gemv_walk_kernel(const GemmArgs p, const 
         const int gi = kt >> gshift;
         sc[s >> 1][j][s & 1] = bload16(rs_s, (uint32_t)n * 2, (uint32_t)(gi * N * 2));
         if (!SYM) zw[s][j] = bload32(rs_z, (uint32_t)(n / 8) * 4, (uint32_t)(gi * (N / 8) * 4));
-      } else {
+      } else if (MODE == kModeE8M0) {
         sb[s][j] = (int)bload8(rs_s, (uint32_t)((lane >> 4) * N + n), (uint32_t)(kt * 4 * N));
+      } else {
+        // groups past K read as 0 from the descriptor's bound (a zero scale)
+#pragma unroll
+        for (int ss = 0; ss < 8; ++ss)
+          nvs[MODE == kModeNV ? s : 0][j][ss >> 1][ss & 1] =
+              (unsigned short)bload8(rs_s, (uint32_t)n, (uint32_t)((kt * 8 + ss) * N));
       }
     }
   };
@@ -205,6 +214,21 @@ __global__ void __launch_bounds__(512) gemv_walk_kernel(const GemmArgs p, const 
     if (MODE == kModeE8M0) {
 #pragma unroll
       for (int j = 0; j < NS; ++j) acc[j] = mfma_f8f4_sb(at, fp4_operand(raw[s][j]), acc[j], sb[s][j]);
+    } else if (MODE == kModeNV) {
+      // 16-wide groups: one MFMA per group on half of a lane's 32-element block (the other half
+      // zeroed), only that block's scale open, then acc += e4m3(scale) * partial
+#pragma unroll
+      for (int j = 0; j < NS; ++j) {
+        const v8i b = fp4_operand(raw[s][j]);
+#pragma unroll
+        for (int ss = 0; ss < 8; ++ss) {
+          const v4f c = mfma_f8f4_sb(at, fp4_half_operand(b, ss), zero4, subgroup_mask_scale(lane, 8, ss));
+          const v2u16 pr = nvs[MODE == kModeNV ? s : 0][j][ss >> 1];
+          const float scf = __builtin_amdgcn_cvt_f32_fp8((int)(uint32_t)pr[ss & 1], 0);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) acc[j][q] = fmaf(scf, c[q], acc[j][q]);
+        }
+      }
     } else if (SYM) {
       const v4f seed = mfma_f8f8(at, splat8(0xB0B0B0B0u), zero4);  // -R/2
 #pragma unroll
@@ -286,6 +310,15 @@ __global__ void __launch_bounds__(512) gemv_walk_kernel(const GemmArgs p, const 
     }
     const float scl = srow[i];
     const int64_t col = sj * kTileN + c;
+    if (MODE == kModeNV) {
+      // the per-output-channel global (f32 bits in the zeros slot)
+      tot *= __int_as_float(p.zeros[col]);
+      if (p.silu) {
+        int64_t su;
+        strip_of(p.silu, g0 + g, j + half, half, NS, nstrips, su);
+        tot_up *= __int_as_float(p.zeros[su * kTileN + c]);
+      }
+    }
     if (p.silu)
       store_out(p, i, col, silu_mul(tot * scl, tot_up * scl, p.out_dtype));
     else
@@ -320,7 +353,6 @@ bool walk_sm(const GemmArgs& p, const WalkPlan& wp, hipStream_t stream) {
     case 4: walk_launch<NS, CH, MODE, SYM, 4>(p, wp, stream); return true;
     case 8: walk_launch<NS, CH, MODE, SYM, 8>(p, wp, stream); return true;
     case 16: walk_launch<NS, CH, MODE, SYM, 16>(p, wp, stream); return true;
-    case 32: walk_launch<NS, CH, MODE, SYM, 32>(p, wp, stream); return true;
     default: return false;
   }
 }
@@ -331,6 +363,7 @@ bool walk_fmt(const GemmArgs& p, const WalkPlan& wp, hipStream_t stream) {
     if (p.zeros == nullptr) return walk_sm<NS, CH, kModeI4, true>(p, wp, stream);
     return walk_sm<NS, CH, kModeI4, false>(p, wp, stream);
   }
+  if (gemv_nvfp4(p)) return walk_sm<NS, CH, kModeNV, false>(p, wp, stream);
   return walk_sm<NS, CH, kModeE8M0, false>(p, wp, stream);
 }
 

@@ -17,16 +17,19 @@ pytestmark = pytest.mark.gpu
 
 # (K, N, format): the configs[1] shapes, configs[0], MXFP4 at configs[5]'s down shape, a 5-wave and
 # a 6-wave K split (threads per row not a power of two), a one-tile K, an N that is not a multiple
-# of 32, and a two-strip weight
+# of 32, a two-strip weight, and NVFP4 (which walks above 4 rows)
 CASES = [(4096, 6144, "sym"), (4096, 4096, "sym"), (4096, 28672, "sym"), (14336, 4096, "sym"),
          (2560, 9728, "asym"), (28672, 8192, "e2m1"), (1536, 768, "e2m1"), (2048, 9600, "sym"),
-         (128, 64, "sym"), (384, 4112, "asym"), (1024, 32, "asym")]
+         (128, 64, "sym"), (384, 4112, "asym"), (1024, 32, "asym"), (8192, 28672, "nvfp4"), (2048, 768, "nvfp4")]
 MS = (1, 2, 3, 4, 5, 7, 8, 9, 13, 16)
 
 
 def _weights(K, N, fmt, dev, seed):
-    e2 = fmt == "e2m1"
-    if e2:
+    e2 = fmt in ("e2m1", "nvfp4")
+    if fmt == "nvfp4":
+        w, s, gl = synth.nvfp4_weight(N, K, seed=seed)
+        z, g = gl, 16
+    elif e2:
         w, s = synth.mxfp4_weight(N, K, seed=seed)
         z, g = None, 32
     else:
@@ -38,9 +41,11 @@ def _weights(K, N, fmt, dev, seed):
 
 
 def _launches(lib, M, K, N, fmt, dtype, silu=False):
-    e2 = fmt == "e2m1"
-    return lib.w4a8_linear_launch_count(M, N, K, 0 if dtype == torch.bfloat16 else 1, 1 if e2 else 0,
-                                        int(fmt == "asym"), int(e2), 32 if e2 else 128, int(silu), 0)
+    e2 = fmt in ("e2m1", "nvfp4")
+    sfmt = 2 if fmt == "nvfp4" else 1 if e2 else 0
+    return lib.w4a8_linear_launch_count(M, N, K, 0 if dtype == torch.bfloat16 else 1, sfmt,
+                                        int(fmt in ("asym", "nvfp4")), int(e2), 16 if fmt == "nvfp4" else 32 if e2 else 128,
+                                        int(silu), 0)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
