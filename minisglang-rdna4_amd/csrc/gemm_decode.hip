@@ -65,9 +65,11 @@ GemvPlan plan_gemv(const GemmArgs& p, int64_t row_blocks, bool quant_src) {
   // narrower dense weights (o_proj, down at 4096 channels) run one strip each, twice the grid
   // (grouped MoE calls keep two: their grids already span the routed experts, except for decode
   // batches of at most 64 slots, whose few blocks hold a row or two each: one strip there, twice
-  // the grid; configs[4] T=1 21.0 -> 19.7 us, T=2 25.4 -> 23.0, T=8 46.7 -> 45.8)
+  // the grid; configs[4] T=1 21.0 -> 19.7 us, T=2 25.4 -> 23.0, T=8 46.7 -> 45.8; and gemm1 (the
+  // silu arm) up to 256 slots, whose blocks hold a few rows: T=16 66.1 -> 62.1 us, T=32 83.7 ->
+  // 80.6, where T=256 measured 126.8 -> 130.8 with one strip)
   pl.nstr = rows > 4 && (p.sorted_ids || strips >= 384) ? 2 : 1;
-  if (p.sorted_ids && p.num_slots <= 64) pl.nstr = 1;
+  if (p.sorted_ids && (p.num_slots <= 64 || (p.silu && p.num_slots <= 256))) pl.nstr = 1;
   // dense: the one-row grid (one strip per workgroup, one row block); grouped: the launched grid
   const int64_t split_groups = p.sorted_ids ? (strips + pl.nstr - 1) / pl.nstr * row_blocks : strips;
   int64_t w, tpw;

@@ -53,14 +53,15 @@ constexpr int kG2cMaxSlots = 16;
 // MODE: kModeI4 (int4, group a multiple of 128), kModeE8M0 (MXFP4), kModeNV (NVFP4). SYM: int4
 // without zero points. KTMAX: most K tiles (weights of every tile are loaded up front). SLOTS: most
 // top-k slots (waves) of the launch, 8 or 16: a 16-wave workgroup leaves each wave 128 VGPRs, an
-// 8-wave one 256, which the 16-tile NVFP4 and asymmetric int4 kernels need.
-template <int MODE, bool SYM, int KTMAX, int SLOTS>
+// 8-wave one 256, which the 16-tile NVFP4 and asymmetric int4 kernels need. NSG: strips per
+// workgroup; each wave quantizes its slot's row once for all of them.
+template <int MODE, bool SYM, int KTMAX, int SLOTS, int NSG>
 __global__ void __launch_bounds__(SLOTS * 64) moe_gemm2_combine_kernel(const G2CArgs p) {
   extern __shared__ __align__(16) unsigned char arows[];  // per wave: KT*128 fp8 codes + 16 bytes
-  __shared__ float ys[SLOTS][kTileN];
+  __shared__ float ys[SLOTS][kTileN * NSG];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // top-k slot j
-  const int strip = blockIdx.x;
+  const int strip0 = blockIdx.x * NSG;
   const int64_t t = blockIdx.y;
   const int64_t slot = t * p.top_k + wave;
   const int pos = p.inv_pos[slot];
@@ -69,8 +70,18 @@ __global__ void __launch_bounds__(SLOTS * 64) moe_gemm2_combine_kernel(const G2C
   const int N = p.N, K = p.K, KT = p.KT;
   const int astride = KT * kTileK + 16;
   unsigned char* arow = arows + wave * astride;
-  const int n = strip * kTileN + (lane & 15);  // this lane's output channel
-  float yv = 0.f;
+  const int nstrips = N / kTileN;
+  // strip q of the workgroup (past the last strip: the last one again, never stored) and this
+  // lane's output channel in it
+  int stq[NSG], nq[NSG];
+#pragma unroll
+  for (int q = 0; q < NSG; ++q) {
+    stq[q] = strip0 + q < nstrips ? strip0 + q : nstrips - 1;
+    nq[q] = stq[q] * kTileN + (lane & 15);
+  }
+  float yv[NSG];
+#pragma unroll
+  for (int q = 0; q < NSG; ++q) yv[q] = 0.f;
 
   if (valid) {
     // ---- the slot's gemm1 row: per-row fp8 quant into this wave's LDS row (act_quant.h's
@@ -96,32 +107,38 @@ __global__ void __launch_bounds__(SLOTS * 64) moe_gemm2_combine_kernel(const G2C
     const BufRsrc rs_s = make_rsrc(scales, (uint32_t)(ngroups * N * kEsz));
     const BufRsrc rs_z = make_rsrc(zeros, (MODE == kModeI4 && zeros) ? (uint32_t)(ngroups * (N / 8) * 4) : 0u);
     const int gshift = 31 - __builtin_clz((unsigned)(p.group >= kTileK ? p.group / kTileK : 1));
-    uint4 raw[KTMAX];
+    uint4 raw[KTMAX][NSG];
     // fp16 scales and NVFP4 block-scale bytes land in the 16-bit halves of their registers (a d16
     // load writes one half without waiting): two scales per VGPR, two NVFP4 bytes per VGPR. Kept
     // as one value per VGPR, the KTMAX=16 NVFP4 and asymmetric int4 kernels spilled to scratch.
     typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
-    v2u16 sc[(KTMAX + 1) / 2];
-    uint32_t zw[(MODE == kModeI4 && !SYM) ? KTMAX : 1];
-    int sb[MODE == kModeE8M0 ? KTMAX : 1];
-    v2u16 nvs[MODE == kModeNV ? KTMAX : 1][4];
+    v2u16 sc[(KTMAX + 1) / 2][NSG];
+    uint32_t zw[(MODE == kModeI4 && !SYM) ? KTMAX : 1][NSG];
+    int sb[MODE == kModeE8M0 ? KTMAX : 1][NSG];
+    v2u16 nvs[MODE == kModeNV ? KTMAX : 1][NSG][4];
     // every slot up to KTMAX is loaded, those past KT from tile KT-1 again (a cache hit, never
     // used): a guard per tile made the compiler finish each tile's scale before issuing the next
     // tile, one memory round trip per K tile
 #pragma unroll
     for (int kt = 0; kt < KTMAX; ++kt) {
       const int kc = kt < KT ? kt : KT - 1;
-      raw[kt] = bload128_nt(rs_w, (uint32_t)lane * 16, (uint32_t)((strip * KT + kc) * kTileBytes));
-      if (MODE == kModeI4) {
-        const int g = kc >> gshift;
-        sc[kt >> 1][kt & 1] = bload16(rs_s, (uint32_t)n * 2, (uint32_t)(g * N * 2));
-        if (!SYM) zw[(MODE == kModeI4 && !SYM) ? kt : 0] = bload32(rs_z, (uint32_t)(n / 8) * 4, (uint32_t)(g * (N / 8) * 4));
-      } else if (MODE == kModeE8M0) {
-        sb[MODE == kModeE8M0 ? kt : 0] = (int)bload8(rs_s, (uint32_t)((lane >> 4) * N + n), (uint32_t)(kc * 4 * N));
-      } else {
 #pragma unroll
-        for (int ss = 0; ss < 8; ++ss)
-          nvs[MODE == kModeNV ? kt : 0][ss >> 1][ss & 1] = (unsigned short)bload8(rs_s, (uint32_t)n, (uint32_t)((kc * 8 + ss) * N));
+      for (int q = 0; q < NSG; ++q) {
+        const int n = nq[q];
+        raw[kt][q] = bload128_nt(rs_w, (uint32_t)lane * 16, (uint32_t)((stq[q] * KT + kc) * kTileBytes));
+        if (MODE == kModeI4) {
+          const int g = kc >> gshift;
+          sc[kt >> 1][q][kt & 1] = bload16(rs_s, (uint32_t)n * 2, (uint32_t)(g * N * 2));
+          if (!SYM)
+            zw[(MODE == kModeI4 && !SYM) ? kt : 0][q] = bload32(rs_z, (uint32_t)(n / 8) * 4, (uint32_t)(g * (N / 8) * 4));
+        } else if (MODE == kModeE8M0) {
+          sb[MODE == kModeE8M0 ? kt : 0][q] = (int)bload8(rs_s, (uint32_t)((lane >> 4) * N + n), (uint32_t)(kc * 4 * N));
+        } else {
+#pragma unroll
+          for (int ss = 0; ss < 8; ++ss)
+            nvs[MODE == kModeNV ? kt : 0][q][ss >> 1][ss & 1] =
+                (unsigned short)bload8(rs_s, (uint32_t)n, (uint32_t)((kc * 8 + ss) * N));
+        }
       }
     }
 
@@ -146,7 +163,9 @@ __global__ void __launch_bounds__(SLOTS * 64) moe_gemm2_combine_kernel(const G2C
 
     // ---- K loop: A row 0 of the MFMA is the slot's row (the other rows are zero and unused)
     const v4f zero4 = v4f{0.f, 0.f, 0.f, 0.f};
-    v4f acc = zero4, tot = zero4;
+    v4f acc[NSG], tot[NSG];
+#pragma unroll
+    for (int q = 0; q < NSG; ++q) acc[q] = tot[q] = zero4;
     const bool arow_lane = (lane & 15) == 0;
 #pragma unroll
     for (int kt = 0; kt < KTMAX; ++kt) {
@@ -160,59 +179,75 @@ __global__ void __launch_bounds__(SLOTS * 64) moe_gemm2_combine_kernel(const G2C
         }
         at[0] = (int)lo.x; at[1] = (int)lo.y; at[2] = (int)lo.z; at[3] = (int)lo.w;
         at[4] = (int)hi.x; at[5] = (int)hi.y; at[6] = (int)hi.z; at[7] = (int)hi.w;
-        if (MODE == kModeE8M0) {
-          acc = mfma_f8f4_sb(at, fp4_operand(raw[kt]), acc, sb[MODE == kModeE8M0 ? kt : 0]);
-        } else if (MODE == kModeI4 && SYM) {
-          const v4f seed = mfma_f8f8(at, splat8(0xB0B0B0B0u), zero4);  // -R/2
-          const v4f c = mfma_f8f8(at, unpack_tile_int4(raw[kt]), seed);
-          const float scf = f16_to_f32(sc[kt >> 1][kt & 1]);
+        const v4f seed = (MODE == kModeI4 && SYM) ? mfma_f8f8(at, splat8(0xB0B0B0B0u), zero4) : zero4;  // -R/2
+        const v4f rh = (MODE == kModeI4 && !SYM) ? mfma_f8f8(at, splat8(kE4M3Half4), zero4) : zero4;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) acc[r] = fmaf(scf, c[r], acc[r]);
-        } else if (MODE == kModeI4) {
-          const v4f rh = mfma_f8f8(at, splat8(kE4M3Half4), zero4);
-          const v4f c = mfma_f8f8(at, unpack_tile_int4(raw[kt]), zero4);
-          const uint32_t z = zw[(MODE == kModeI4 && !SYM) ? kt : 0];
-          const float coef = 15.0f - 2.0f * (float)((z >> (4 * (n & 7))) & 15u);
-          const float scf = f16_to_f32(sc[kt >> 1][kt & 1]);
+        for (int q = 0; q < NSG; ++q) {
+          if (MODE == kModeE8M0) {
+            acc[q] = mfma_f8f4_sb(at, fp4_operand(raw[kt][q]), acc[q], sb[MODE == kModeE8M0 ? kt : 0][q]);
+          } else if (MODE == kModeI4 && SYM) {
+            const v4f c = mfma_f8f8(at, unpack_tile_int4(raw[kt][q]), seed);
+            const float scf = f16_to_f32(sc[kt >> 1][q][kt & 1]);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) acc[r] = fmaf(scf, fmaf(coef, rh[r], c[r]), acc[r]);
-        } else {
-          const v8i b = fp4_operand(raw[kt]);
+            for (int r = 0; r < 4; ++r) acc[q][r] = fmaf(scf, c[r], acc[q][r]);
+          } else if (MODE == kModeI4) {
+            const v4f c = mfma_f8f8(at, unpack_tile_int4(raw[kt][q]), zero4);
+            const uint32_t z = zw[(MODE == kModeI4 && !SYM) ? kt : 0][q];
+            const float coef = 15.0f - 2.0f * (float)((z >> (4 * (nq[q] & 7))) & 15u);
+            const float scf = f16_to_f32(sc[kt >> 1][q][kt & 1]);
 #pragma unroll
-          for (int ss = 0; ss < 8; ++ss) {
-            const v4f c = mfma_f8f4_sb(at, fp4_half_operand(b, ss), zero4, subgroup_mask_scale(lane, 8, ss));
-            const float scf = __builtin_amdgcn_cvt_f32_fp8((int)(uint32_t)nvs[MODE == kModeNV ? kt : 0][ss >> 1][ss & 1], 0);
+            for (int r = 0; r < 4; ++r) acc[q][r] = fmaf(scf, fmaf(coef, rh[r], c[r]), acc[q][r]);
+          } else {
+            const v8i b = fp4_operand(raw[kt][q]);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) acc[r] = fmaf(scf, c[r], acc[r]);
+            for (int ss = 0; ss < 8; ++ss) {
+              const v4f c = mfma_f8f4_sb(at, fp4_half_operand(b, ss), zero4, subgroup_mask_scale(lane, 8, ss));
+              const float scf =
+                  __builtin_amdgcn_cvt_f32_fp8((int)(uint32_t)nvs[MODE == kModeNV ? kt : 0][q][ss >> 1][ss & 1], 0);
+#pragma unroll
+              for (int r = 0; r < 4; ++r) acc[q][r] = fmaf(scf, c[r], acc[q][r]);
+            }
           }
         }
         // end of a run of the grouped gemm2's split: fold it into the total in run order
         if ((kt + 1) % p.tpw == 0 || kt + 1 == KT) {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) tot[r] = tot[r] + acc[r];
-          acc = zero4;
+          for (int q = 0; q < NSG; ++q) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) tot[q][r] = tot[q][r] + acc[q][r];
+            acc[q] = zero4;
+          }
         }
       }
     }
     // row 0 of the C fragment: element 0 of lanes 0..15 (column = lane)
-    float v = tot[0];
-    if (MODE == kModeNV) v *= __int_as_float(zeros[n]);  // the per-output-channel global
-    yv = v * s;
-    if (p.row_dtype != kF32) yv = from_dtype(to_dtype(yv, p.row_dtype), p.row_dtype);
-  }
-  if (lane < kTileN) ys[wave][lane] = yv;
-  __syncthreads();
-  if (threadIdx.x < kTileN) {
-    float acc = 0.f;
-    for (int j = 0; j < p.top_k; ++j) {
-      const int64_t sl = t * p.top_k + j;
-      if (p.inv_pos[sl] >= 0) acc = fmaf(p.tw[sl], ys[j][threadIdx.x], acc);
+#pragma unroll
+    for (int q = 0; q < NSG; ++q) {
+      float v = tot[q][0];
+      if (MODE == kModeNV) v *= __int_as_float(zeros[nq[q]]);  // the per-output-channel global
+      yv[q] = v * s;
+      if (p.row_dtype != kF32) yv[q] = from_dtype(to_dtype(yv[q], p.row_dtype), p.row_dtype);
     }
-    const int64_t col = (int64_t)strip * kTileN + threadIdx.x;
-    if (p.out_dtype == kF32)
-      reinterpret_cast<float*>(p.out)[t * p.ldo + col] = acc;
-    else
-      reinterpret_cast<uint16_t*>(p.out)[t * p.ldo + col] = to_dtype(acc, p.out_dtype);
+  }
+  if (lane < kTileN) {
+#pragma unroll
+    for (int q = 0; q < NSG; ++q) ys[wave][q * kTileN + lane] = yv[q];
+  }
+  __syncthreads();
+  if (threadIdx.x < kTileN * NSG) {
+    const int q = threadIdx.x / kTileN, c = threadIdx.x % kTileN;
+    if (strip0 + q < nstrips) {
+      float acc = 0.f;
+      for (int j = 0; j < p.top_k; ++j) {
+        const int64_t sl = t * p.top_k + j;
+        if (p.inv_pos[sl] >= 0) acc = fmaf(p.tw[sl], ys[j][threadIdx.x], acc);
+      }
+      const int64_t col = (int64_t)(strip0 + q) * kTileN + c;
+      if (p.out_dtype == kF32)
+        reinterpret_cast<float*>(p.out)[t * p.ldo + col] = acc;
+      else
+        reinterpret_cast<uint16_t*>(p.out)[t * p.ldo + col] = to_dtype(acc, p.out_dtype);
+    }
   }
 }
 
@@ -227,17 +262,27 @@ bool moe_gemm2_combine_fits(int64_t K, int scale_fmt, bool has_zeros, int wfmt, 
   return fmt && wide_ok && K % kTileK == 0 && K <= 16 * kTileK && top_k >= 1 && top_k <= kG2cMaxSlots;
 }
 
+// The 8-tile, 8-slot kernel (the configs[4] decode shape) takes two strips per workgroup from 8
+// tokens on: each wave quantizes its slot's row once for both and keeps twice the weight bytes in
+// flight (configs[4], whole call: T=8 39.8 -> 38.5 us, T=12 55.7 -> 54.7, T=16 64.0 -> 62.9); below
+// 8 tokens the grid of half as many workgroups leaves CUs idle (T=1 15.5 -> 16.9). Four strips
+// were slower at every T. Each strip's arithmetic is the same, so the bits are too.
 template <int MODE, bool SYM>
-static void g2c_launch(const G2CArgs& a, dim3 grid, dim3 block, size_t lds, hipStream_t st) {
+static void g2c_launch(const G2CArgs& a, int64_t T, size_t lds, hipStream_t st) {
   const bool few = a.top_k <= 8;
-  if (a.KT <= 8 && few)
-    hipLaunchKernelGGL((moe_gemm2_combine_kernel<MODE, SYM, 8, 8>), grid, block, lds, st, a);
+  const int nstrips = a.N / kTileN;
+  const dim3 block((unsigned)(a.top_k * 64));
+  auto grid = [&](int nsg) { return dim3((unsigned)((nstrips + nsg - 1) / nsg), (unsigned)T); };
+  if (a.KT <= 8 && few && T >= 8)
+    hipLaunchKernelGGL((moe_gemm2_combine_kernel<MODE, SYM, 8, 8, 2>), grid(2), block, lds, st, a);
+  else if (a.KT <= 8 && few)
+    hipLaunchKernelGGL((moe_gemm2_combine_kernel<MODE, SYM, 8, 8, 1>), grid(1), block, lds, st, a);
   else if (a.KT <= 8)
-    hipLaunchKernelGGL((moe_gemm2_combine_kernel<MODE, SYM, 8, 16>), grid, block, lds, st, a);
+    hipLaunchKernelGGL((moe_gemm2_combine_kernel<MODE, SYM, 8, 16, 1>), grid(1), block, lds, st, a);
   else if (few)
-    hipLaunchKernelGGL((moe_gemm2_combine_kernel<MODE, SYM, 16, 8>), grid, block, lds, st, a);
+    hipLaunchKernelGGL((moe_gemm2_combine_kernel<MODE, SYM, 16, 8, 1>), grid(1), block, lds, st, a);
   else if constexpr (MODE != kModeNV && (MODE != kModeI4 || SYM))
-    hipLaunchKernelGGL((moe_gemm2_combine_kernel<MODE, SYM, 16, 16>), grid, block, lds, st, a);
+    hipLaunchKernelGGL((moe_gemm2_combine_kernel<MODE, SYM, 16, 16, 1>), grid(1), block, lds, st, a);
 }
 
 // p: the grouped gemm2's arguments as w4a8_moe_gemm would build them for the decode arm (for the
@@ -255,13 +300,11 @@ int launch_moe_gemm2_combine(const GemmArgs& p, int64_t row_blocks, const uint16
   g.zeros = p.zeros; g.z_expert_stride = p.z_expert_stride;
   g.group = p.group; g.N = (int)p.N; g.K = (int)p.K; g.KT = (int)p.KT; g.tpw = tpw;
   g.out = p.out; g.out_dtype = p.out_dtype; g.ldo = p.ldo; g.row_dtype = row_dtype;
-  const dim3 grid((unsigned)(p.N / kTileN), (unsigned)T);
-  const dim3 block((unsigned)(p.top_k * 64));
   const size_t lds = (size_t)p.top_k * (p.KT * kTileK + 16);
-  if (p.wfmt == kE2M1 && p.sfmt == kScaleE8M0) g2c_launch<kModeE8M0, false>(g, grid, block, lds, stream);
-  else if (p.wfmt == kE2M1) g2c_launch<kModeNV, false>(g, grid, block, lds, stream);
-  else if (p.zeros == nullptr) g2c_launch<kModeI4, true>(g, grid, block, lds, stream);
-  else g2c_launch<kModeI4, false>(g, grid, block, lds, stream);
+  if (p.wfmt == kE2M1 && p.sfmt == kScaleE8M0) g2c_launch<kModeE8M0, false>(g, T, lds, stream);
+  else if (p.wfmt == kE2M1) g2c_launch<kModeNV, false>(g, T, lds, stream);
+  else if (p.zeros == nullptr) g2c_launch<kModeI4, true>(g, T, lds, stream);
+  else g2c_launch<kModeI4, false>(g, T, lds, stream);
   return hipGetLastError() == hipSuccess ? kOk : kErrHip;
 }
 
