@@ -319,7 +319,7 @@ def configs_leg(kernels, dev) -> dict:
     """The other BASELINE configs through the product's operator API, weights rotated over more
     than twice the 256 MB MALL for the bandwidth-bound cases: cfg1 (AWQ zero-point int4 g128,
     M=16, K=2560, N=9728), cfg4 (MoE E=128 top-8 H=2048 I=768, int4 g128 fp16 scales, T in
-    {1,16,256,4096}) and cfg5 (MXFP4 E8M0 block-32 at K=8192,N=28672 and K=28672,N=8192, M in
+    {1,16,32,256,4096}) and cfg5 (MXFP4 E8M0 block-32 at K=8192,N=28672 and K=28672,N=8192, M in
     {1,16,4096}). Bytes and FLOPs count the algorithmic traffic (codes, scales, zero words,
     bf16 activations in and out; MoE: the distinct experts the route selected)."""
     import torch
@@ -370,7 +370,7 @@ def configs_leg(kernels, dev) -> dict:
         s2 = (torch.randn(E, I // g, H, generator=gen, device=dev).abs() * 0.02 + 1e-4).to(torch.float16)
         layers.append((w13, s13, w2, s2))
     per_expert = 2 * I * H // 2 + (H // g) * 2 * I * 2 + H * I // 2 + (I // g) * H * 2
-    for T in (1, 16, 256, 4096):
+    for T in (1, 16, 32, 256, 4096):
         x = make_x(T, H, 400 + T, dev)
         logits = torch.randn(T, E, generator=gen, device=dev).to(torch.bfloat16)
         distinct = int(torch.topk(logits.float(), k, dim=-1).indices.unique().numel())
