@@ -398,8 +398,17 @@ moe_prep_kernel(const void* __restrict__ logits, int ldtype, int64_t T, int E, i
     return;
   }
   __shared__ int32_t ids_s[kPrepMaxSlots];
-  for (int64_t t = threadIdx.x >> 6; t < T; t += kPrepThreads / 64)
-    route_token<PER>(logits, ldtype, t, E, top_k, renorm, tw, ids, ids_s);
+  // one token per wave, 16 at a time; past 16 tokens with 16-bit logits two per wave (token t and
+  // t + 16), whose routes run interleaved
+  constexpr int kW = kPrepThreads / 64;
+  for (int64_t t = threadIdx.x >> 6; t < T; t += 2 * kW) {
+    if (t + kW < T && ldtype != kF32) {
+      route_token_pair<PER>(logits, ldtype, t, t + kW, E, top_k, renorm, tw, ids, ids_s);
+    } else {
+      route_token<PER>(logits, ldtype, t, E, top_k, renorm, tw, ids, ids_s);
+      if (t + kW < T) route_token<PER>(logits, ldtype, t + kW, E, top_k, renorm, tw, ids, ids_s);
+    }
+  }
   lds_barrier();
   if (slots) {
     const int S = (int)(T * top_k);

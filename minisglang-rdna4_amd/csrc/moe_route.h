@@ -88,9 +88,62 @@ struct RoutePick {
   int myid;
 };
 
+// 16-bit logits (bf16, fp16): the same order in one 32-bit key, the logit's 16 bits mapped the same
+// way in the high half and ~e in the low half (E < 65536), so each reduction step is one unsigned
+// maximum instead of a 64-bit compare and two selects. 0: no candidate, as above (a mapped value
+// of 0 would be the bits 0xffff, a NaN).
+__device__ __forceinline__ uint32_t route_key16(uint32_t raw, int dtype, int e, bool ok) {
+  const float v = from_dtype((uint16_t)raw, dtype);
+  uint32_t b = raw & 0xffffu;
+  b = b == 0x8000u ? 0u : b;
+  const uint32_t u = (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
+  return (ok && v == v) ? (u << 16) | (0xffffu - (uint32_t)e) : 0u;
+}
+__device__ __forceinline__ float route_key16_logit(uint32_t k, int dtype) {
+  const uint32_t u = k >> 16;
+  const uint32_t b = (u & 0x8000u) ? (u & 0x7fffu) : (~u & 0xffffu);
+  return from_dtype((uint16_t)b, dtype);
+}
+template <int CTRL, int RM = 0xf>
+__device__ __forceinline__ uint32_t key16_max_step(uint32_t k) {
+  uint32_t o;
+  if constexpr (RM == 0xf) o = (uint32_t)__builtin_amdgcn_mov_dpp((int)k, CTRL, 0xf, 0xf, false);
+  else o = (uint32_t)__builtin_amdgcn_update_dpp((int)k, (int)k, CTRL, RM, 0xf, false);
+  return o > k ? o : k;
+}
+__device__ __forceinline__ uint32_t wave_key16_max(uint32_t k) {
+  k = key16_max_step<kDppXor1>(k);
+  k = key16_max_step<kDppXor2>(k);
+  k = key16_max_step<kDppHalfMirror>(k);
+  k = key16_max_step<kDppRowMirror>(k);
+  k = key16_max_step<kDppRowBcast15, 0xa>(k);
+  k = key16_max_step<kDppRowBcast31, 0xc>(k);
+  return (uint32_t)__builtin_amdgcn_readlane((int)k, 63);
+}
+
 template <int PER>
 __device__ __forceinline__ RoutePick route_pick(const uint32_t (&raw)[PER], int dtype, int E, int n) {
   const int lane = threadIdx.x & 63;
+  if (dtype != kF32) {
+    uint32_t key[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int e = lane + 64 * i;
+      key[i] = route_key16(raw[i], dtype, e, e < E);
+    }
+    uint32_t mine = 0;
+    for (int j = 0; j < n; ++j) {
+      uint32_t m = key[0];
+#pragma unroll
+      for (int i = 1; i < PER; ++i) m = key[i] > m ? key[i] : m;
+      const uint32_t top = wave_key16_max(m);
+#pragma unroll
+      for (int i = 0; i < PER; ++i) key[i] = key[i] == top ? 0u : key[i];
+      mine = lane == j ? top : mine;
+    }
+    if (mine == 0u) return RoutePick{-INFINITY, 0x7fffffff};
+    return RoutePick{route_key16_logit(mine, dtype), (int)(0xffffu - (mine & 0xffffu))};
+  }
   uint64_t key[PER];
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
@@ -156,6 +209,62 @@ __device__ __forceinline__ void route_token(const void* __restrict__ logits, int
     tw[t * top_k + lane] = w;
     ids[t * top_k + lane] = r.myid;
     if (ids_s) ids_s[t * top_k + lane] = r.myid;
+  }
+}
+
+// Two tokens per wave with 16-bit logits: the two routes' selection rounds, softmax reductions and
+// weights are independent chains, so the wave runs them interleaved in about the time of one
+// (each token's results are route_token's bits).
+template <int PER>
+__device__ __forceinline__ void route_token_pair(const void* __restrict__ logits, int dtype, int64_t t0, int64_t t1,
+                                                 int E, int top_k, int renorm, float* __restrict__ tw,
+                                                 int32_t* __restrict__ ids, int32_t* ids_s) {
+  const int lane = threadIdx.x & 63;
+  uint32_t raw0[PER], raw1[PER];
+  route_load<PER>(logits, dtype, t0, E, raw0);
+  route_load<PER>(logits, dtype, t1, E, raw1);
+  uint32_t k0[PER], k1[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int e = lane + 64 * i;
+    k0[i] = route_key16(raw0[i], dtype, e, e < E);
+    k1[i] = route_key16(raw1[i], dtype, e, e < E);
+  }
+  uint32_t mine0 = 0, mine1 = 0;
+  for (int j = 0; j < top_k; ++j) {
+    uint32_t m0 = k0[0], m1 = k1[0];
+#pragma unroll
+    for (int i = 1; i < PER; ++i) {
+      m0 = k0[i] > m0 ? k0[i] : m0;
+      m1 = k1[i] > m1 ? k1[i] : m1;
+    }
+    const uint32_t top0 = wave_key16_max(m0), top1 = wave_key16_max(m1);
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      k0[i] = k0[i] == top0 ? 0u : k0[i];
+      k1[i] = k1[i] == top1 ? 0u : k1[i];
+    }
+    mine0 = lane == j ? top0 : mine0;
+    mine1 = lane == j ? top1 : mine1;
+  }
+  const RoutePick r0 = mine0 == 0u ? RoutePick{-INFINITY, 0x7fffffff}
+                                   : RoutePick{route_key16_logit(mine0, dtype), (int)(0xffffu - (mine0 & 0xffffu))};
+  const RoutePick r1 = mine1 == 0u ? RoutePick{-INFINITY, 0x7fffffff}
+                                   : RoutePick{route_key16_logit(mine1, dtype), (int)(0xffffu - (mine1 & 0xffffu))};
+  float mx0, sum0, mx1, sum1;
+  route_softmax<PER>(raw0, dtype, E, mx0, sum0);
+  route_softmax<PER>(raw1, dtype, E, mx1, sum1);
+  const float w0 = route_weight(r0, mx0, sum0, top_k, renorm);
+  const float w1 = route_weight(r1, mx1, sum1, top_k, renorm);
+  if (lane < top_k) {
+    tw[t0 * top_k + lane] = w0;
+    ids[t0 * top_k + lane] = r0.myid;
+    tw[t1 * top_k + lane] = w1;
+    ids[t1 * top_k + lane] = r1.myid;
+    if (ids_s) {
+      ids_s[t0 * top_k + lane] = r0.myid;
+      ids_s[t1 * top_k + lane] = r1.myid;
+    }
   }
 }
 
