@@ -130,6 +130,32 @@ def test_e8m0_health_report():
     assert info["would_saturate_fp16"] == 2 and info["e8m0_nan_groups"] == 0 and info["exp_max"] == 40
 
 
+def test_e8m0_health_report_against_brute_force():
+    """Every field against a per-code count over all 256 codes (0 = the 2^-127 zero code, 255 = NaN,
+    codes outside fp16's normal exponents -14..15 saturate, code 0 excepted)."""
+    mx = pkg("quant.mxfp4")
+    g = torch.Generator().manual_seed(7)
+    for lo, hi in [(0, 256), (100, 140), (120, 130), (0, 2), (250, 256)]:
+        scale = torch.randint(lo, hi, (3, 40, 24), generator=g, dtype=torch.int32).to(torch.uint8)
+        v = scale.numpy().astype(np.int64).ravel()
+        e = v - 127
+        info = mx.e8m0_scale_health(scale)
+        assert info["exp_min"] == e.min() and info["exp_max"] == e.max()
+        assert info["e8m0_nan_groups"] == int((v == 255).sum())
+        assert info["e8m0_zero_code_groups"] == int((v == 0).sum())
+        assert info["would_saturate_fp16"] == int(((e > 15) | ((e < -14) & (v != 0))).sum())
+
+
+def test_mxfp4_word_view_is_the_nibble_repack():
+    """The converters' word view equals packing the unpacked nibbles explicitly (code j at bits 4j)."""
+    mx = pkg("quant.mxfp4")
+    g = torch.Generator().manual_seed(9)
+    packed = torch.randint(0, 256, (3, 48, 64), generator=g, dtype=torch.int32).to(torch.uint8)
+    words = mx.convert_mxfp4_moe_e8m0(packed, torch.full((3, 48, 4), 127, dtype=torch.uint8))["w_packed"]
+    for i in range(3):
+        assert torch.equal(words[i], mx.pack_codes_to_int32(mx.unpack_e2m1_nibbles(packed[i])))
+
+
 # ------------------------------------------------------------------------------------ W4 tiles
 def tile_reference(w_packed: np.ndarray, K: int, e2m1: bool) -> np.ndarray:
     """numpy restatement of the W4 tile layout: (N/16, KT, 64 lanes, 16 bytes)."""
