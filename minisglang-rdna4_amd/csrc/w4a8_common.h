@@ -100,13 +100,15 @@ __device__ __forceinline__ v8i splat8(uint32_t v) {
 
 // bf16 / fp16 scalar helpers (RNE)
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
+// Round to nearest even; a NaN keeps its sign and top payload bits and is made quiet ((u >> 16) |
+// 0x40). gfx950's v_cvt_pk_bf16_f32, which the __bf16 conversion compiles to, gives exactly these
+// bits: checked on the GPU against the integer form ((u + 0x7fff + ((u >> 16) & 1)) >> 16, the NaN
+// select) over all 65536 upper halves with 8 lower halves each (ties, subnormals, NaN payloads) and
+// 2^25 random patterns, no difference. One instruction instead of six. The empty asm pins f as an
+// f32 value, as for fp16 below.
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  // round to nearest even; NaN keeps its top bits and is made quiet. Written as a select so that a
-  // conversion costs no branch.
-  const uint32_t u = __float_as_uint(f);
-  const uint32_t rne = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-  const uint32_t nan = (u >> 16) | 0x40u;
-  return (uint16_t)(((u & 0x7fffffffu) > 0x7f800000u) ? nan : rne);
+  asm volatile("" : "+v"(f));
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
 }
 __device__ __forceinline__ float f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 // The empty asm pins f as an f32 value: without it the compiler may contract a producing f32
