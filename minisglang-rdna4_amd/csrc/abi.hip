@@ -22,6 +22,7 @@ int launch_moe_gemm2_combine(const GemmArgs& p, int64_t row_blocks, const uint16
 size_t gemv_workspace_bytes(int64_t M, int64_t N, int64_t K, int grouped, int64_t row_blocks);
 int launch_prefill(const GemmArgs& p, int64_t rows_to_cover, int bm_rows, hipStream_t stream);
 int launch_prefill_lds(const GemmArgs& p, int64_t rows_to_cover, int bm_rows, hipStream_t stream);
+int launch_prefill_dma(const GemmArgs& p, int64_t rows_to_cover, int bm_rows, hipStream_t stream);
 int launch_moe_route(const void* logits, int dtype, int64_t T, int E, int top_k, int renorm, float* tw,
                      int32_t* ids, hipStream_t stream);
 int launch_moe_align(const int32_t* ids, int64_t numel, int E, int bm, int64_t P, int32_t* sorted_ids,
@@ -358,6 +359,16 @@ int w4a16_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, 
   const bool decode = kernel == 1 || (kernel == 0 && M <= kGemvMaxRows);
   if (decode) {
     rc = hip_status(launch_gemv(p, (p.M + 15) / 16, false, st), "w4a16_linear(decode)");
+  } else if (x_dtype == kBF16 && aligned16(out) && ldo % 8 == 0) {
+    // bf16 on the DMA-staged kernel: its epilogue sums each row's two terms (and applies silu)
+    // and writes the bf16 rows itself, the same arithmetic as the f32 rows + sum kernel below
+    GemmArgs q = p;
+    q.out = out; q.ldo = ldo; q.out_dtype = kBF16; q.silu = silu; q.tsum2 = 1;
+    rc = launch_prefill_dma(q, q.M, 0, st);
+    if (rc != kErrUnsupported) return hip_status(rc, "w4a16_linear(prefill, term sum)");
+    rc = launch_prefill_lds(p, p.M, 0, st);
+    if (rc == kErrUnsupported) rc = launch_prefill(p, p.M, 128, st);
+    rc = hip_status(rc, "w4a16_linear(prefill)");
   } else {
     rc = launch_prefill_lds(p, p.M, 0, st);
     if (rc == kErrUnsupported) rc = launch_prefill(p, p.M, 128, st);

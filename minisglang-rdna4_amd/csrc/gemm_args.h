@@ -55,6 +55,9 @@ struct GemmArgs {
   int out_dtype;
   int64_t ldo;        // elements
   int silu;           // 1: out[:, j] = silu(y[:, j]) * y[:, j + N/2]
+  // 1: rows 2m and 2m+1 are the two fp8 terms of bf16 activation row m (W4A16): out row m is
+  // bf16((0 + y[2m]) + y[2m+1]), silu applied to those sums (prefill DMA kernel only)
+  int tsum2;
   // split-K
   float* partial;     // (SK, M, N) f32 when SK > 1
   int SK;

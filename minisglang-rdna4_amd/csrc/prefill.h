@@ -157,6 +157,72 @@ __device__ __forceinline__ void store_tile_lds(const GemmArgs& p, const v4f (&ac
   }
 }
 
+// One W4A16 bf16 output value from its two term rows: y_t = acc_t * s_t rounded to f32 as the f32
+// output of the split GEMM stores them, then (0 + y_0) + y_1 as the term-sum kernel adds them (the
+// empty asm keeps the products from contracting into the additions).
+__device__ __forceinline__ float tsum2_value(float a0, float s0, float a1, float s1) {
+  float y0 = a0 * s0, y1 = a1 * s1;
+  asm volatile("" : "+v"(y0), "+v"(y1));
+  return (0.0f + y0) + y1;
+}
+
+// The W4A16 bf16 epilogue (p.tsum2): the lane's rows 4q + r hold term r & 1 of activation row
+// 2q + (r >> 1) of the block's 8, so each lane sums its own row pairs and writes bf16 token rows
+// (silu over the summed gate and up, rounded as the fused silu arms round) through the per-wave LDS
+// tile as store_tile_lds does: 8 token rows per 16-row block. row0: the wave's first term row
+// (even); token rows are row / 2.
+template <bool SILU, int RB, int NSB>
+__device__ __forceinline__ void store_tile_tsum2(const GemmArgs& p, const v4f (&acc)[RB][NSB], const float (&sc)[RB][4],
+                                                 uint32_t valid, int64_t row0, int lane, int64_t col0, int nvs,
+                                                 unsigned char* scr) {
+  constexpr int JN = SILU ? NSB / 2 : NSB;
+  constexpr int E = 2;
+  constexpr int W = JN * 16 * E;
+  constexpr int P = W + 16;
+  constexpr int CPR = W / 16;
+  constexpr int RPI = 64 / CPR;
+  static_assert(CPR <= 64 && 64 % CPR == 0 && (RPI >= 8 || 8 % RPI == 0), "chunk layout");
+  const int q = lane >> 4, c = lane & 15;
+  const int crow = lane / CPR, chunk = lane % CPR;
+  const bool cok = chunk * 16 / (16 * E) < nvs;
+  unsigned char* outb = reinterpret_cast<unsigned char*>(p.out) + col0 * E + chunk * 16;
+  const int64_t trow0 = row0 / 2;
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float s0 = sc[rb][2 * h], s1 = sc[rb][2 * h + 1];
+#pragma unroll
+      for (int j = 0; j < JN; ++j) {
+        float v;
+        if constexpr (SILU)
+          v = lsilu_mul(tsum2_value(acc[rb][j][2 * h], s0, acc[rb][j][2 * h + 1], s1),
+                        tsum2_value(acc[rb][j + NSB / 2][2 * h], s0, acc[rb][j + NSB / 2][2 * h + 1], s1), kBF16);
+        else
+          v = tsum2_value(acc[rb][j][2 * h], s0, acc[rb][j][2 * h + 1], s1);
+        *reinterpret_cast<uint16_t*>(scr + (2 * q + h) * P + j * 16 * E + c * E) = to_dtype(v, kBF16);
+      }
+    }
+    // token rows of this block that hold data: bit 2q + h from row 4q + 2h of any lane of group q
+    uint32_t rv = 0;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint64_t b = __ballot((valid >> (rb * 4 + 2 * h)) & 1u);
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) rv |= (uint32_t)((b >> (16 * qq)) & 1u) << (2 * qq + h);
+    }
+#pragma unroll
+    for (int i = 0; i < (8 + RPI - 1) / RPI; ++i) {
+      const int rr = i * RPI + crow;
+      const uint4 d = *reinterpret_cast<const uint4*>(scr + (rr < 8 ? rr : 7) * P + chunk * 16);
+      if (cok && rr < 8 && ((rv >> rr) & 1u)) {
+        const int64_t trow = trow0 + rb * 8 + rr;
+        *reinterpret_cast<uint4*>(outb + trow * p.ldo * E) = d;
+      }
+    }
+  }
+}
+
 // Every row's source lookup and activation scale is loaded before the first store: a load issued
 // between stores makes the wait for its value also wait for all the stores issued before it (one
 // vector-memory counter covers both), which serialized the whole epilogue.
@@ -206,6 +272,11 @@ __device__ __forceinline__ void store_tile_scaled(const GemmArgs& p, const v4f (
       nvs += (j < jn && ok) ? 1 : 0;
     }
     const int64_t col0 = (int64_t)gs0 * kTileN;
+    if (p.tsum2) {  // the host sets it for bf16 output rows with 16-byte aligned stride only
+      if (p.silu) store_tile_tsum2<true>(p, acc, sc, valid, row0, lane, col0, nvs, scr);
+      else store_tile_tsum2<false>(p, acc, sc, valid, row0, lane, col0, nvs, scr);
+      return;
+    }
     if (p.out_dtype == kBF16) {
       if (p.silu) store_tile_lds<kBF16, true>(p, acc, sc, valid, row0, lane, col0, nvs, scr);
       else store_tile_lds<kBF16, false>(p, acc, sc, valid, row0, lane, col0, nvs, scr);

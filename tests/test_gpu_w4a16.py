@@ -98,6 +98,38 @@ def test_w4a16_silu_bit_exact(kernels, dev, dtype, fmt):
         assert torch.equal(fused, ref), f"{fmt} {dtype} M={M}: max {(fused.float() - ref.float()).abs().max().item():.3e}"
 
 
+def _split_rows_f32(q, sc, tiles, s, z, g, N, K, e2):
+    """The fp8 GEMM of the split rows with f32 output, through the C ABI's prefill arm."""
+    abi = pkg("_abi")
+    lib = abi.load()
+    y = torch.empty((q.shape[0], N), dtype=torch.float32, device=q.device)
+    sfmt = abi.SCALE_F16 if s.dtype == torch.float16 else abi.SCALE_E8M0
+    abi.check(lib.w4a8_gemm(abi.ptr(q), K, abi.ptr(sc), q.shape[0], abi.ptr(tiles), N, K, abi.ptr(s), sfmt,
+                            abi.ptr(z), abi.W_E2M1 if e2 else abi.W_INT4, g, abi.ptr(y), abi.F32, N, 0, None, 0,
+                            abi.KERNEL_PREFILL, abi.stream_of(q)), "w4a8_gemm")
+    return y
+
+
+@pytest.mark.parametrize("fmt", ["sym", "asym", "mxfp4"])
+def test_w4a16_bf16_term_sum_in_epilogue(kernels, dev, fmt):
+    """bf16 prefill: the GEMM's epilogue adds each row's two fp8 terms and rounds once. Bit-identical
+    to the arm composed from its pieces: w4a16_act_split, the fp8 GEMM writing the terms' f32 rows,
+    and (0 + y[2m]) + y[2m+1] in f32 rounded to bf16 (the sum the decode arm's kernel takes)."""
+    K, N = 1024, 512
+    w, s, z, g, e2 = _case(fmt, N, K, seed=31)
+    tiles = kernels.repack_w4(w.to(dev), weight_is_e2m1=e2)
+    sd, zd = s.to(dev), None if z is None else z.to(dev)
+    for M in (17, 64, 300):
+        x = (synth.activations(M, K, seed=M + 3, outliers=True, dtype=torch.float32) * 0.5).to(torch.bfloat16).to(dev)
+        x[1, :16] = 0.0
+        out = kernels.w4a16_linear(x, tiles, sd, zd, g, N, weight_is_e2m1=e2)
+        q, sc = kernels.w4a16_act_split(x)
+        y = _split_rows_f32(q, sc, tiles, sd, zd, g, N, K, e2)
+        ref = ((0.0 + y[0::2]) + y[1::2]).to(torch.bfloat16)
+        _sync()
+        assert torch.equal(out, ref), f"{fmt} M={M}: max {(out.float() - ref.float()).abs().max().item():.3e}"
+
+
 @pytest.mark.parametrize("fmt", ["sym", "mxfp4"])
 def test_w4a16_no_further_from_exact_than_w4a8(kernels, oracle, dev, fmt):
     """tests/w4a16_e2m1_parity_test.py:119-129 of the reference, directionally: against the
