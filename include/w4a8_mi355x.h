@@ -82,7 +82,11 @@ int w4a8_gemm(const uint8_t* x_fp8, int64_t ldx, const float* act_scales, int64_
               void* stream);
 
 /* Workspace bytes w4a8_linear may need for M rows of K inputs (the fp8 codes and scales of x when
- * they are not produced inside the GEMM kernel); -1 on bad sizes. */
+ * they are not produced inside the GEMM kernel; for prefill calls of 1024 rows or more, also the
+ * codes again in the GEMM's operand order with one row-sum seed per row and 128 inputs, which wide
+ * symmetric int4 weights use); -1 on bad sizes. w4a8_linear also accepts a workspace of just the
+ * codes and scales (M * K and 4 * M bytes, each rounded up to 256): such calls run the GEMM on the
+ * row-major codes, with the same outputs. */
 int64_t w4a8_linear_workspace_bytes(int64_t M, int64_t K);
 
 /* Dense W4A8 linear on bf16/fp16 activations x (M, ldx): per-token fp8 quant of x, then the GEMM of
@@ -100,7 +104,9 @@ int w4a8_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, c
 
 /* Kernel launches a w4a8_linear call of these shapes and formats makes: 1 when the per-token quant
  * runs inside the GEMV (decode calls whose rows the GEMV quantizes itself), 2 when an act-quant
- * launch comes first; 0 for M = 0; minus the status code on bad arguments. Host-only (no device
+ * launch comes first, 3 when the prefill GEMM also takes the codes rewritten in its operand order
+ * (symmetric int4, 1024 rows or more, N >= 16384, with the full w4a8_linear_workspace_bytes);
+ * 0 for M = 0; minus the status code on bad arguments. Host-only (no device
  * call), for callers that budget launches per step. No counterpart in the reference, whose in-op
  * quant is always a separate launch (python/minisgl/quant/kernels.py:1512-1515). */
 int w4a8_linear_launch_count(int64_t M, int64_t N, int64_t K, int x_dtype, int scale_fmt, int has_zeros, int wfmt,

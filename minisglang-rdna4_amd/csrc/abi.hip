@@ -5,6 +5,7 @@
 // allocates device memory: outputs and workspaces come from the caller.
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 
 #include "gemm_args.h"
 #include "../../include/w4a8_mi355x.h"
@@ -42,6 +43,8 @@ int launch_rms_norm(const void* x, int64_t ldx, void* res, int64_t ldr, const vo
 int w4a16_terms(int dtype);
 int launch_act_split(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx, uint8_t* q, int64_t ldq,
                      float* scales, hipStream_t stream);
+int launch_act_tile(const uint8_t* q, int64_t ldq, int64_t M, int64_t K, uint8_t* qt, float* seeds,
+                    int64_t seeds_ld, hipStream_t stream);
 int launch_tsum(const float* y, int64_t N, int64_t M, int dtype, void* out, int64_t ldo, int silu, hipStream_t st);
 int64_t w4a16_moe_max_inter();
 int launch_moe_silu_split(const float* y, int64_t ldy, const int32_t* inv_pos, int64_t T, int top_k, int64_t I,
@@ -79,6 +82,26 @@ static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 static const int kGemvMaxRows = 16;
 
+// Dense symmetric int4 prefill calls of at least W4A8_PREFILL_TILED rows (default 1024; 0 turns it
+// off) on weights of at least 16384 output channels that the DMA-staged kernel takes (its own
+// checks, launch_prefill_dma): their codes are rewritten in that kernel's operand order with the
+// row-sum seeds, which it then reads instead of computing them (act_tile_kernel). The rewrite costs a
+// launch and a pass over the codes; what it saves grows with the column tiles that read each row
+// block (M=2048 / 8192, K=4096: N=28672 5-7% faster, N=4096 and 6144 1-5% slower).
+static int64_t tiled_min_rows() {
+  static const int64_t min_rows = [] {
+    const char* e = getenv("W4A8_PREFILL_TILED");
+    return e ? (int64_t)atoll(e) : (int64_t)1024;
+  }();
+  return min_rows;
+}
+static bool dma_tiled_ok(const GemmArgs& p) {
+  const int64_t min_rows = tiled_min_rows();
+  const bool sym4 = p.wfmt == kInt4 && p.sfmt == kScaleF16 && p.group % 128 == 0 && !p.zeros;
+  return min_rows > 0 && p.M >= min_rows && p.N >= 16384 && sym4 && p.K % 128 == 0 && p.KT >= 3 && !(p.silu && (p.N / 16) % 2) &&
+         p.N * p.KT * 64 < ((int64_t)1 << 31) && p.M * p.K < ((int64_t)1 << 31);
+}
+
 // Bound on align blocks that can hold routed rows: every expert with rows contributes
 // ceil(rows/bm) blocks, so at most numel/bm + min(E, numel) of them are non-empty.
 static int64_t moe_max_blocks(int64_t numel, int64_t E, int bm, int64_t P) {
@@ -112,6 +135,22 @@ static int check_weights(const char* who, int64_t N, int64_t K, int scale_fmt, c
     return fail(kErrInvalid, "%s: E8M0 scales are per 32-element block (group_size=32), got %lld", who, (long long)group);
   return kOk;
 }
+
+// w4a8_linear's workspace: the row-major codes and scales of x (what every call needs), then for
+// the calls that may take the tiled prefill (tiled_min_rows) the codes of whole 16-row blocks in
+// the GEMM's operand order and one row-sum seed per row and K tile. A workspace of only the first
+// part is accepted; such calls run the row-major GEMM, with the same results.
+static int64_t round256(int64_t b);
+static int64_t linear_ws_rowmajor(int64_t M, int64_t K) { return round256(M * K) + round256(M * 4); }
+static int64_t linear_ws_tiled(int64_t M, int64_t K) {
+  const int64_t min_rows = tiled_min_rows();
+  if (min_rows <= 0 || M < min_rows) return 0;
+  const int64_t Mp = (M + 15) / 16 * 16, KT = (K + 127) / 128;
+  return round256(Mp * K) + round256(KT * Mp * 4);
+}
+namespace w4a8 {
+int64_t linear_workspace_min(int64_t M, int64_t K) { return M < 0 || K <= 0 ? -1 : linear_ws_rowmajor(M, K); }
+}  // namespace w4a8
 
 extern "C" {
 
@@ -228,7 +267,7 @@ int w4a8_gemm(const uint8_t* x_fp8, int64_t ldx, const float* act_scales, int64_
 
 int64_t w4a8_linear_workspace_bytes(int64_t M, int64_t K) {
   if (M < 0 || K <= 0) return -1;
-  return round256(M * K) + round256(M * 4);
+  return linear_ws_rowmajor(M, K) + linear_ws_tiled(M, K);
 }
 
 int w4a8_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const void* w_tile, int64_t N,
@@ -249,7 +288,7 @@ int w4a8_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, c
   if (decode && gemv_can_fuse_quant(p, (M + 15) / 16))
     return hip_status(launch_gemv(p, (M + 15) / 16, true, st), "w4a8_linear(decode, fused quant)");
   // quantize into the workspace, then the fp8 GEMM
-  const int64_t need = w4a8_linear_workspace_bytes(M, K);
+  const int64_t need = linear_ws_rowmajor(M, K);
   if (workspace == nullptr || workspace_bytes < need || !aligned16(workspace))
     return fail(kErrInvalid, "w4a8_linear: needs a 16-byte aligned workspace of %lld bytes, got %lld", (long long)need,
                 (long long)workspace_bytes);
@@ -257,6 +296,20 @@ int w4a8_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, c
   float* xs = reinterpret_cast<float*>(xq + round256(M * K));
   rc = launch_act_quant(x, x_dtype, M, K, ldx, xq, K, xs, nullptr, st);
   if (rc) return hip_status(rc, "w4a8_linear(act quant)");
+  if (!decode && dma_tiled_ok(p) && workspace_bytes >= need + linear_ws_tiled(M, K)) {
+    // prefill on the DMA-staged kernel: the codes again in its operand order, with the seeds
+    const int64_t Mp = (M + 15) / 16 * 16;
+    uint8_t* xt = reinterpret_cast<uint8_t*>(xs) + round256(M * 4);
+    float* seeds = reinterpret_cast<float*>(xt + round256(Mp * K));
+    rc = launch_act_tile(xq, K, M, K, xt, seeds, Mp, st);
+    if (rc) return hip_status(rc, "w4a8_linear(act tile)");
+    GemmArgs q = p;
+    q.xsrc = nullptr;
+    q.xq = xt; q.ldx = K; q.act_scales = xs;
+    q.a_tiled = 1; q.seeds = seeds; q.seeds_ld = Mp;
+    rc = launch_prefill_dma(q, M, 0, st);
+    if (rc != kErrUnsupported) return hip_status(rc, "w4a8_linear(prefill, tiled)");
+  }
   p.xsrc = nullptr;
   p.xq = xq; p.ldx = K; p.act_scales = xs;
   return run_dense("w4a8_linear", p, kernel, st);
@@ -277,7 +330,8 @@ int w4a8_linear_launch_count(int64_t M, int64_t N, int64_t K, int x_dtype, int s
   if (M == 0) return 0;
   const bool decode = kernel == 1 || (kernel == 0 && M <= kGemvMaxRows);
   p.xsrc = reinterpret_cast<const uint16_t*>(fake); p.ldxs = K; p.xdtype = x_dtype;
-  return decode && gemv_can_fuse_quant(p, (M + 15) / 16) ? 1 : 2;
+  if (decode) return gemv_can_fuse_quant(p, (M + 15) / 16) ? 1 : 2;
+  return dma_tiled_ok(p) ? 3 : 2;
 }
 
 }  // extern "C"

@@ -47,6 +47,55 @@ act_quant_wave_kernel(const uint16_t* __restrict__ x, int64_t ldx, int64_t M, in
     quant_row_wave<CPW>(x + m * ldx, K, dtype, q + m * ldq, scales + m, lane);
 }
 
+// The codes of act_quant_kernel rewritten for the dense prefill GEMM in its A-operand order: per
+// 16-row block and 128-wide K tile one 2 KiB block at ((row / 16) * KT + kt) * 2048 whose two 1 KiB
+// halves hold, at lane l * 16, row (l & 15)'s bytes [16 (l >> 4), +16) and [64 + 16 (l >> 4), +16) of
+// the tile -- what the GEMM's operand read gives lane l, so its LDS-DMA copies whole 1 KiB runs
+// instead of 64-byte pieces of 16 rows. With them, per block and K tile, the GEMM's row-sum seed (the
+// e4m3 -0.5 splat MFMA on that operand: the same instruction on the same bytes, so the same bits) at
+// seeds[kt * seeds_ld + row], seeds_ld = M rounded up to 16. Rows past M in the last block are zero
+// codes. One wave per (block, K tile), four per workgroup; every lane active at the MFMA.
+__global__ void __launch_bounds__(256)
+act_tile_kernel(const uint8_t* __restrict__ q, int64_t ldq, int64_t M, int KT, uint8_t* __restrict__ qt,
+                float* __restrict__ seeds, int64_t seeds_ld) {
+  const int lane = threadIdx.x & 63;
+  const int64_t nblk = (M + 15) / 16;
+  const int64_t units = nblk * KT;
+  const int r = lane & 15, qd = lane >> 4;
+  for (int64_t u = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); u < units; u += (int64_t)gridDim.x * 4) {
+    const int64_t blk = u / KT;
+    const int kt = (int)(u - blk * KT);
+    const int64_t m = blk * 16 + r;
+    const uint8_t* src = q + (m < M ? m : 0) * ldq + (int64_t)kt * kTileK + 16 * qd;
+    const uint4 z = make_uint4(0, 0, 0, 0);
+    const uint4 h0 = m < M ? *reinterpret_cast<const uint4*>(src) : z;
+    const uint4 h1 = m < M ? *reinterpret_cast<const uint4*>(src + 64) : z;
+    uint8_t* dst = qt + u * 2048 + lane * 16;
+    *reinterpret_cast<uint4*>(dst) = h0;
+    *reinterpret_cast<uint4*>(dst + 1024) = h1;
+    v8i a;
+    a[0] = (int)h0.x; a[1] = (int)h0.y; a[2] = (int)h0.z; a[3] = (int)h0.w;
+    a[4] = (int)h1.x; a[5] = (int)h1.y; a[6] = (int)h1.z; a[7] = (int)h1.w;
+    v4f pre = mfma_f8f8(a, splat8(0xB0B0B0B0u), v4f{0.f, 0.f, 0.f, 0.f});
+    asm volatile("" : "+v"(pre));  // the MFMA runs with every lane active, before the lane branch
+    // output lane l holds rows 4 (l >> 4) + i of column l & 15; column 0's lanes store them
+    if (r == 0)
+      *reinterpret_cast<float4*>(seeds + (int64_t)kt * seeds_ld + blk * 16 + 4 * qd) =
+          make_float4(pre[0], pre[1], pre[2], pre[3]);
+  }
+}
+
+int launch_act_tile(const uint8_t* q, int64_t ldq, int64_t M, int64_t K, uint8_t* qt, float* seeds,
+                    int64_t seeds_ld, hipStream_t stream) {
+  if (M <= 0) return kOk;
+  const int KT = (int)(K / kTileK);
+  const int64_t units = (M + 15) / 16 * KT;
+  const int64_t wgs = (units + 3) / 4;
+  const dim3 g((unsigned)(wgs < 65536 ? wgs : 65536)), b(256);
+  hipLaunchKernelGGL(act_tile_kernel, g, b, 0, stream, q, ldq, M, KT, qt, seeds, seeds_ld);
+  return hipGetLastError() == hipSuccess ? kOk : kErrHip;
+}
+
 int launch_act_quant(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx, uint8_t* q,
                      int64_t ldq, float* scales, const int32_t* row_count, hipStream_t stream) {
   if (M <= 0) return kOk;

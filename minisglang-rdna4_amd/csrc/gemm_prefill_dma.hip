@@ -23,7 +23,7 @@
 
 namespace w4a8 {
 
-template <int WM, int WN, int RB, int NSB, int MODE>
+template <int WM, int WN, int RB, int NSB, int MODE, bool AT>
 __global__ void __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 gemm_dma_kernel(const GemmArgs p) {
   constexpr int T = WM * WN * 64, NW = WM * WN;
@@ -38,12 +38,17 @@ gemm_dma_kernel(const GemmArgs p) {
   // E8M0 bytes: one 256-byte slot per strip (a wave's dword DMA covers 64 lanes x 4 bytes; lanes
   // 0-15 carry the strip's 64 bytes, the rest repeat them into the slot's unused tail)
   constexpr int kSE8 = NSTRIP * 256;
-  constexpr int kStage = kFp4 ? S::kA + S::kB + kSE8 : S::kBytes;
+  // AT (p.a_tiled): A in operand order, and for symmetric int4 the row-sum seeds travel by LDS-DMA
+  // (one dword per row, kSeedB bytes per stage) instead of four MFMAs per wave and step
+  constexpr bool kSeedL = AT && MODE == kPSym;
+  constexpr int kSeedOff = kFp4 ? S::kA + S::kB + kSE8 : S::kBytes;
+  constexpr int kSeedB = kSeedL ? BM * 4 : 0;
+  constexpr int kStage = kSeedOff + kSeedB;
   static_assert(!kFp4 || B_DMA * NW == NSTRIP, "fp4 strips / waves");
   constexpr int B_PER = kFp4 ? 0 : NSTRIP * 64 / T;    // int4 16-byte chunks per thread per step
   static_assert(kFp4 || B_PER * T == NSTRIP * 64, "int4 chunks / threads");
   // vector-memory operations every wave issues per step (all unconditional, so one count holds)
-  constexpr int NOPS = kFp4 ? S_DMA + A_PER + B_DMA : A_PER + B_PER + 1 + (MODE == kPAsym ? 1 : 0);
+  constexpr int NOPS = (kFp4 ? S_DMA + A_PER + B_DMA : A_PER + B_PER + 1 + (MODE == kPAsym ? 1 : 0)) + (kSeedL ? 1 : 0);
 
   __shared__ __align__(16) unsigned char st0[kStage];
   __shared__ __align__(16) unsigned char st1[kStage];
@@ -110,13 +115,31 @@ gemm_dma_kernel(const GemmArgs p) {
   // ---- per-lane source offsets (fixed across K steps; the step adds a scalar offset)
   // A block b = wave + i*NW of a step is row block b/2, half b%2; lane l reads row (l & 15) of it,
   // bytes [64*half + 16*(l >> 4), +16) of the step's 128
+  // AT: block b's 1 KiB sits whole in the tiled codes (row blocks past M read the last one)
   uint32_t a_voff[A_PER];
+  const int64_t nblk16 = (p.M + 15) / 16;
 #pragma unroll
   for (int i = 0; i < A_PER; ++i) {
     const int b = wave + i * NW;
-    int64_t ar;
-    const bool ok = lrow_source(p, blk_row0 + (b >> 1) * 16 + (lane & 15), ar);
-    a_voff[i] = (uint32_t)((ok ? ar : 0) * p.ldx) + (b & 1) * 64 + 16 * (lane >> 4);
+    if constexpr (AT) {
+      int64_t rbg = blk_row0 / 16 + (b >> 1);
+      rbg = rbg < nblk16 ? rbg : nblk16 - 1;
+      a_voff[i] = (uint32_t)((rbg * KT * 2 + (b & 1)) * 1024 + lane * 16);
+    } else {
+      int64_t ar;
+      const bool ok = lrow_source(p, blk_row0 + (b >> 1) * 16 + (lane & 15), ar);
+      a_voff[i] = (uint32_t)((ok ? ar : 0) * p.ldx) + (b & 1) * 64 + 16 * (lane >> 4);
+    }
+  }
+  // seeds: wave w copies rows 64 (w % (BM / 64)) + lane of the tile (waves past BM / 64 copy the same
+  // rows again, so every wave issues one DMA per step and one vmcnt count holds)
+  constexpr int kSeedW = BM / 64 > 0 ? BM / 64 : 1;
+  const BufRsrc rs_seed = make_rsrc(p.seeds, kSeedL ? (uint32_t)((size_t)KT * p.seeds_ld * 4) : 0u);
+  uint32_t seed_voff = 0;
+  if constexpr (kSeedL) {
+    int64_t sr = blk_row0 + 64 * (wave % kSeedW) + lane;
+    sr = sr < p.seeds_ld ? sr : p.seeds_ld - 1;
+    seed_voff = (uint32_t)(sr * 4);
   }
   // The epilogue's rows: one per thread, its source looked up in the same round trip as the A
   // rows' and its act scale loaded ahead of step 0's loads; both go to LDS at the end of the
@@ -183,11 +206,14 @@ gemm_dma_kernel(const GemmArgs p) {
         lds_dma4(rs_s, st + S::kA + S::kB + (wave + i * NW) * 256, e_voff[i],
                  (uint32_t)__builtin_amdgcn_readfirstlane(kt * 4 * N));
     }
-    const uint32_t so_a = (uint32_t)__builtin_amdgcn_readfirstlane(kt * kTileK);
+    const uint32_t so_a = (uint32_t)__builtin_amdgcn_readfirstlane(AT ? kt * 2048 : kt * kTileK);
     if (part & 1) {
 #pragma unroll
       for (int i = 0; i < A_PER; ++i)
         lds_dma16(rs_a, st + (wave + i * NW) * 1024, a_voff[i], so_a);
+      if constexpr (kSeedL)
+        lds_dma4(rs_seed, st + kSeedOff + (wave % kSeedW) * 256, seed_voff,
+                 (uint32_t)__builtin_amdgcn_readfirstlane(kt * (int)p.seeds_ld * 4));
     }
     if constexpr (kFp4) {
 #pragma unroll
@@ -269,8 +295,12 @@ gemm_dma_kernel(const GemmArgs p) {
       for (int rb = 0; rb < RB; ++rb) a[rb] = lds_operand(st + oa + rb * 2048, 0);
       v4f pre[RB];
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb)  // symmetric: -R/2; zero points: +R/2
-        pre[rb] = mfma_f8f8(a[rb], splat8(MODE == kPSym ? 0xB0B0B0B0u : kE4M3Half4), zero4);
+      for (int rb = 0; rb < RB; ++rb) {  // symmetric: -R/2; zero points: +R/2
+        if constexpr (kSeedL)
+          pre[rb] = *reinterpret_cast<const v4f*>(st + kSeedOff + (wm * RB * 16 + rb * 16 + 4 * (lane >> 4)) * 4);
+        else
+          pre[rb] = mfma_f8f8(a[rb], splat8(MODE == kPSym ? 0xB0B0B0B0u : kE4M3Half4), zero4);
+      }
       v4f cp[RB];
       float scp = 0.f, cfp = 0.f;
       v8i bn = lds_operand(st + ob, 0);
@@ -412,8 +442,8 @@ gemm_dma_kernel(const GemmArgs p) {
                     [&](int j, bool& ok) __attribute__((always_inline)) { return gstrip(wn * NSB + j, ok); }, scr);
 }
 
-template <int WM, int WN, int RB, int NSB, int MODE>
-static int launch_dma_cfg(const GemmArgs& p, int64_t row_tiles, hipStream_t stream) {
+template <int WM, int WN, int RB, int NSB, int MODE, bool AT = false>
+static int launch_dma_cfg_at(const GemmArgs& p, int64_t row_tiles, hipStream_t stream) {
   constexpr int BN = WN * NSB * 16;
   const int64_t ncols = p.silu ? p.N / 2 : p.N;
   const int64_t colw = p.silu ? BN / 2 : BN;
@@ -423,9 +453,16 @@ static int launch_dma_cfg(const GemmArgs& p, int64_t row_tiles, hipStream_t stre
     while ((gx * gy) % 8) ++gy;
   const dim3 grid((unsigned)gx, (unsigned)gy);
   const dim3 block(WM * WN * 64);
-  auto kern = gemm_dma_kernel<WM, WN, RB, NSB, MODE>;
+  auto kern = gemm_dma_kernel<WM, WN, RB, NSB, MODE, AT>;
   hipLaunchKernelGGL(kern, grid, block, 0, stream, p);
   return hipGetLastError() == hipSuccess ? kOk : kErrHip;
+}
+
+// dense calls with p.a_tiled take the tiled-A instantiation; grouped calls never set it
+template <int WM, int WN, int RB, int NSB, int MODE>
+static int launch_dma_cfg(const GemmArgs& p, int64_t row_tiles, hipStream_t stream) {
+  if (p.a_tiled) return launch_dma_cfg_at<WM, WN, RB, NSB, MODE, true>(p, row_tiles, stream);
+  return launch_dma_cfg_at<WM, WN, RB, NSB, MODE, false>(p, row_tiles, stream);
 }
 
 template <int WM, int WN, int RB, int NSB>
@@ -433,6 +470,13 @@ static int launch_dma_modes(const GemmArgs& p, int mode, int64_t row_tiles, hipS
   if (mode == kPSym) return launch_dma_cfg<WM, WN, RB, NSB, kPSym>(p, row_tiles, stream);
   if (mode == kPAsym) return launch_dma_cfg<WM, WN, RB, NSB, kPAsym>(p, row_tiles, stream);
   return launch_dma_cfg<WM, WN, RB, NSB, kPE8M0>(p, row_tiles, stream);
+}
+// grouped tiles (row-major A gathered through the sorted ids): no tiled-A instantiation
+template <int WM, int WN, int RB, int NSB>
+static int launch_dma_modes_grouped(const GemmArgs& p, int mode, int64_t row_tiles, hipStream_t stream) {
+  if (mode == kPSym) return launch_dma_cfg_at<WM, WN, RB, NSB, kPSym>(p, row_tiles, stream);
+  if (mode == kPAsym) return launch_dma_cfg_at<WM, WN, RB, NSB, kPAsym>(p, row_tiles, stream);
+  return launch_dma_cfg_at<WM, WN, RB, NSB, kPE8M0>(p, row_tiles, stream);
 }
 
 // Formats and shapes as launch_prefill_lds, plus at least three K steps (the pipeline's depth).
@@ -461,8 +505,9 @@ int launch_prefill_dma(const GemmArgs& p, int64_t rows_to_cover, int bm_rows, hi
   // in LDS and its accumulators are the only per-step state, so it takes 64 x 128 wave tiles
   // (256 x 256 per workgroup: a quarter less LDS read per MFMA than 64 x 64); int4 holds the
   // unpacked fp8 weights plus the partials of its per-group scaling and stays at 64 x 64.
-  if (bm_rows == 64) return launch_dma_modes<2, 4, 2, 2>(p, mode, (rows_to_cover + 63) / 64, stream);
-  if (bm_rows == 128) return launch_dma_modes<2, 4, 4, 4>(p, mode, (rows_to_cover + 127) / 128, stream);
+  if (p.a_tiled && (p.sorted_ids || bm_rows)) return kErrUnsupported;
+  if (bm_rows == 64) return launch_dma_modes_grouped<2, 4, 2, 2>(p, mode, (rows_to_cover + 63) / 64, stream);
+  if (bm_rows == 128) return launch_dma_modes_grouped<2, 4, 4, 4>(p, mode, (rows_to_cover + 127) / 128, stream);
   // Grids of at most half a workgroup per CU take smaller tiles. int4: 128 x 128 when that gives
   // 192 or more workgroups, else 64 x 128 (the configs[2] M=512 calls, M=1024 on 4096-wide
   // weights): K=4096 N=6144 M=512 39.5 -> 29.9 us, K=4096 N=4096 M=1024 42.4 -> 32.4 us, K=14336

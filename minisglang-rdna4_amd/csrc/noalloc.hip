@@ -20,7 +20,8 @@
 #include "../../include/w4a8_mi355x.h"
 
 namespace w4a8 {
-int set_last_error(int code, const char* msg);  // abi.hip
+int set_last_error(int code, const char* msg);       // abi.hip
+int64_t linear_workspace_min(int64_t M, int64_t K);  // abi.hip: the row-major part w4a8_linear accepts
 }
 
 static constexpr int64_t kScratchBytes = 64ll << 20;  // 64 MiB per device
@@ -73,7 +74,9 @@ int64_t w4a8_linear_noalloc_max_bytes(void) { return kScratchBytes; }
 int w4a8_linear_noalloc(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const void* w_tile, int64_t N,
                         const void* scales, int scale_fmt, const int32_t* zeros, int wfmt, int64_t group_size,
                         void* out, int out_dtype, int64_t ldo, int silu, int kernel, void* stream) {
-  const int64_t need = w4a8_linear_workspace_bytes(M, K);
+  // the scratch holds at least the row-major codes and scales; a prefill call that would also take
+  // the tiled copy falls back to the row-major GEMM (the same results) when that does not fit
+  const int64_t need = w4a8::linear_workspace_min(M, K);
   if (need < 0) return failf(1, "w4a8_linear_noalloc: bad sizes M=%lld K=%lld", (long long)M, (long long)K);
   if (need > kScratchBytes)
     return failf(1,

@@ -326,6 +326,29 @@ def test_producer_pair_bit_identical(kernels, dev, M):
     assert torch.equal(base, pre) and torch.equal(base, pre8)
 
 
+@pytest.mark.parametrize("fmt,M,K,N", [("sym", 2048, 4096, 28672), ("sym", 1100, 1024, 16400), ("sym", 300, 1024, 512),
+                                        ("asym", 1100, 1024, 16384), ("mxfp4", 1024, 4096, 1024)])
+def test_prefill_tiled_quant_matches_row_major(kernels, dev, fmt, M, K, N):
+    """Wide symmetric int4 prefill calls that quantize x themselves rewrite the codes in the GEMM's
+    operand order with the row-sum seeds (a third launch), which the GEMM reads instead of computing;
+    callers' own (x_fp8, act_scales) pairs reach the GEMM row by row and it computes the seeds. Both
+    give the same bits (also on a ragged 1025-strip weight and the row-major formats beside them)."""
+    x = synth.activations(M, K, seed=M + K, outliers=True).to(dev)
+    if fmt == "mxfp4":
+        w, s = synth.mxfp4_weight(N, K, seed=N + 1)
+        z, g, e2 = None, 32, True
+    else:
+        w, s, z = synth.int4_weight(N, K, 128, seed=N + 1, asym=fmt == "asym", scale_floor=1e-4)
+        g, e2 = 128, False
+    tiles = kernels.repack_w4(w.to(dev), weight_is_e2m1=e2)
+    sd, zd = s.to(dev), None if z is None else z.to(dev)
+    q, sc = kernels.act_quant(x)
+    base = kernels.w4a8_linear(x, tiles, sd, zd, g, weight_is_e2m1=e2)
+    pre = kernels.w4a8_linear(x, tiles, sd, zd, g, weight_is_e2m1=e2, x_fp8=q, act_scales=sc)
+    _sync()
+    assert torch.equal(base, pre), f"{fmt} M={M}: max {(base.float() - pre.float()).abs().max().item():.3e}"
+
+
 def test_dispatch_ledger_records_arms(kernels, dev):
     eng = pkg("_hip_engage")
     K, N, g = 1024, 128, 128
