@@ -418,6 +418,18 @@ int w4a16_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, 
     // and writes the bf16 rows itself, the same arithmetic as the f32 rows + sum kernel below
     GemmArgs q = p;
     q.out = out; q.ldo = ldo; q.out_dtype = kBF16; q.silu = silu; q.tsum2 = 1;
+    if (dma_tiled_ok(q)) {
+      // wide symmetric int4: the terms' codes rewritten in the GEMM's operand order with their
+      // row-sum seeds, into the f32 rows' space that this path leaves unused
+      const int64_t Mp = round16(q.M), KT = q.KT;
+      uint8_t* xt = reinterpret_cast<uint8_t*>(y);
+      float* seeds = reinterpret_cast<float*>(xt + round256(Mp * K));
+      if (round256(Mp * K) + round256(KT * Mp * 4) <= round256(T * M * N * 4)) {
+        rc = launch_act_tile(xq, ldq, q.M, K, xt, seeds, Mp, st);
+        if (rc) return hip_status(rc, "w4a16_linear(act tile)");
+        q.xq = xt; q.ldx = K; q.a_tiled = 1; q.seeds = seeds; q.seeds_ld = Mp;
+      }
+    }
     rc = launch_prefill_dma(q, q.M, 0, st);
     if (rc != kErrUnsupported) return hip_status(rc, "w4a16_linear(prefill, term sum)");
     rc = launch_prefill_lds(p, p.M, 0, st);
