@@ -67,7 +67,11 @@ int64_t w4a8_tile_bytes(int64_t N, int64_t K);
  * (python/minisgl/quant/mxfp4.py:134-206), whose (N, K/8) int32 output is this call's input. */
 int w4a8_repack_weights(const int32_t* w_packed, int64_t N, int64_t K, int wfmt, void* w_tile, void* stream);
 
-/* Workspace bytes w4a8_gemm needs for (M, N, K) and a kernel choice (0 auto, 1 decode, 2 prefill). */
+/* Workspace bytes w4a8_gemm may use for (M, N, K) and a kernel choice (0 auto, 1 decode, 2 prefill);
+ * -1 on bad sizes. Prefill calls of 1024 rows or more on 16384+ output channels: room for the codes
+ * rewritten in the GEMM's operand order with one row-sum seed per row and 128 inputs, which symmetric
+ * int4 weights take (a launch before the GEMM); without it the GEMM reads the row-major codes, with
+ * the same outputs. */
 int64_t w4a8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int kernel);
 
 /* Dense W4A8 GEMM: out[m, n] = act_scales[m] * sum_g scale[g, n] * sum_{k in g} e4m3(x[m,k]) * w(n,k).

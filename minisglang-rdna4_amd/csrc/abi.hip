@@ -203,7 +203,10 @@ int w4a8_repack_weights(const int32_t* w_packed, int64_t N, int64_t K, int wfmt,
 }
 
 int64_t w4a8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int kernel) {
-  if (kernel == 2 || (kernel == 0 && M > kGemvMaxRows)) return 0;
+  if (M < 0 || N <= 0 || K <= 0) return -1;
+  // prefill: room for the codes rewritten in the GEMM's operand order with their row-sum seeds,
+  // which wide symmetric int4 weights take (the call runs without it too, on the row-major codes)
+  if (kernel == 2 || (kernel == 0 && M > kGemvMaxRows)) return N >= 16384 ? linear_ws_tiled(M, K) : 0;
   return (int64_t)gemv_workspace_bytes(M, N, K, 0, (M + 15) / 16);
 }
 
@@ -253,7 +256,6 @@ int w4a8_gemm(const uint8_t* x_fp8, int64_t ldx, const float* act_scales, int64_
               int64_t K, const void* scales, int scale_fmt, const int32_t* zeros, int wfmt, int64_t group_size,
               void* out, int out_dtype, int64_t ldo, int silu, void* workspace, int64_t workspace_bytes, int kernel,
               void* stream) {
-  (void)workspace; (void)workspace_bytes;
   GemmArgs p;
   int rc = dense_args("w4a8_gemm", M, w_tile, N, K, scales, scale_fmt, zeros, wfmt, group_size, out, out_dtype, ldo,
                       silu, kernel, p);
@@ -262,7 +264,21 @@ int w4a8_gemm(const uint8_t* x_fp8, int64_t ldx, const float* act_scales, int64_
   if (ldx < K || ldx % 16 || !aligned16(x_fp8))
     return fail(kErrInvalid, "w4a8_gemm: x_fp8 rows must be 16-byte aligned with stride >= K (ldx=%lld)", (long long)ldx);
   p.xq = x_fp8; p.ldx = ldx; p.act_scales = act_scales;
-  return run_dense("w4a8_gemm", p, kernel, (hipStream_t)stream);
+  const hipStream_t st = (hipStream_t)stream;
+  const bool decode = kernel == 1 || (kernel == 0 && M <= kGemvMaxRows);
+  if (!decode && dma_tiled_ok(p) && workspace && aligned16(workspace) && workspace_bytes >= linear_ws_tiled(M, K)) {
+    // the caller's codes rewritten in the GEMM's operand order with their seeds (as w4a8_linear)
+    const int64_t Mp = (M + 15) / 16 * 16;
+    uint8_t* xt = reinterpret_cast<uint8_t*>(workspace);
+    float* seeds = reinterpret_cast<float*>(xt + round256(Mp * K));
+    rc = launch_act_tile(x_fp8, ldx, M, K, xt, seeds, Mp, st);
+    if (rc) return hip_status(rc, "w4a8_gemm(act tile)");
+    GemmArgs q = p;
+    q.xq = xt; q.ldx = K; q.a_tiled = 1; q.seeds = seeds; q.seeds_ld = Mp;
+    rc = launch_prefill_dma(q, M, 0, st);
+    if (rc != kErrUnsupported) return hip_status(rc, "w4a8_gemm(prefill, tiled)");
+  }
+  return run_dense("w4a8_gemm", p, kernel, st);
 }
 
 int64_t w4a8_linear_workspace_bytes(int64_t M, int64_t K) {

@@ -320,10 +320,13 @@ def _dense(x, w_packed, scales, w_zeros, group_size, weight_is_e2m1, x_fp8, act_
             what,
         )
     else:
+        # prefill calls on wide weights may rewrite the codes in the GEMM's operand order first
+        ws_bytes = int(lib.w4a8_gemm_workspace_bytes(M, N, K, arm))
+        ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=x.device) if ws_bytes > 0 else None
         _abi.check(
             lib.w4a8_gemm(_abi.ptr(xq), K, _abi.ptr(xs), M, _abi.ptr(tiles), N, K, _abi.ptr(sc), sfmt, zeros, wfmt,
-                          group_size, _abi.ptr(out), _abi.dtype_code(x.dtype), nout, int(silu), None, 0, arm,
-                          _abi.stream_of(x)),
+                          group_size, _abi.ptr(out), _abi.dtype_code(x.dtype), nout, int(silu), _abi.ptr(ws),
+                          max(ws_bytes, 0), arm, _abi.stream_of(x)),
             what,
         )
     return out, tiles is not w_packed
