@@ -108,9 +108,7 @@ int w4a8_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, c
 
 /* Kernel launches a w4a8_linear call of these shapes and formats makes: 1 when the per-token quant
  * runs inside the GEMV (decode calls whose rows the GEMV quantizes itself), 2 when an act-quant
- * launch comes first, 3 when the prefill GEMM also takes the codes rewritten in its operand order
- * (symmetric int4, 1024 rows or more, N >= 16384, with the full w4a8_linear_workspace_bytes);
- * 0 for M = 0; minus the status code on bad arguments. Host-only (no device
+ * launch comes first; 0 for M = 0; minus the status code on bad arguments. Host-only (no device
  * call), for callers that budget launches per step. No counterpart in the reference, whose in-op
  * quant is always a separate launch (python/minisgl/quant/kernels.py:1512-1515). */
 int w4a8_linear_launch_count(int64_t M, int64_t N, int64_t K, int x_dtype, int scale_fmt, int has_zeros, int wfmt,

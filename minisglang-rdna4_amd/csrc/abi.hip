@@ -45,6 +45,8 @@ int launch_act_split(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx
                      float* scales, hipStream_t stream);
 int launch_act_tile(const uint8_t* q, int64_t ldq, int64_t M, int64_t K, uint8_t* qt, float* seeds,
                     int64_t seeds_ld, hipStream_t stream);
+int launch_act_quant_tiled(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx, uint8_t* qt, float* scales,
+                           float* seeds, int64_t seeds_ld, hipStream_t stream);
 int launch_tsum(const float* y, int64_t N, int64_t M, int dtype, void* out, int64_t ldo, int silu, hipStream_t st);
 int64_t w4a16_moe_max_inter();
 int launch_moe_silu_split(const float* y, int64_t ldy, const int32_t* inv_pos, int64_t T, int top_k, int64_t I,
@@ -95,10 +97,17 @@ static int64_t tiled_min_rows() {
   }();
   return min_rows;
 }
-static bool dma_tiled_ok(const GemmArgs& p) {
+static int64_t tiled_min_n() {
+  static const int64_t n = [] {
+    const char* e = getenv("W4A8_PREFILL_TILED_N");
+    return e ? (int64_t)atoll(e) : (int64_t)16384;
+  }();
+  return n;
+}
+static bool dma_tiled_ok(const GemmArgs& p, int64_t min_n = 16384) {
   const int64_t min_rows = tiled_min_rows();
   const bool sym4 = p.wfmt == kInt4 && p.sfmt == kScaleF16 && p.group % 128 == 0 && !p.zeros;
-  return min_rows > 0 && p.M >= min_rows && p.N >= 16384 && sym4 && p.K % 128 == 0 && p.KT >= 3 && !(p.silu && (p.N / 16) % 2) &&
+  return min_rows > 0 && p.M >= min_rows && p.N >= min_n && sym4 && p.K % 128 == 0 && p.KT >= 3 && !(p.silu && (p.N / 16) % 2) &&
          p.N * p.KT * 64 < ((int64_t)1 << 31) && p.M * p.K < ((int64_t)1 << 31);
 }
 
@@ -310,15 +319,13 @@ int w4a8_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, c
                 (long long)workspace_bytes);
   uint8_t* xq = reinterpret_cast<uint8_t*>(workspace);
   float* xs = reinterpret_cast<float*>(xq + round256(M * K));
-  rc = launch_act_quant(x, x_dtype, M, K, ldx, xq, K, xs, nullptr, st);
-  if (rc) return hip_status(rc, "w4a8_linear(act quant)");
-  if (!decode && dma_tiled_ok(p) && workspace_bytes >= need + linear_ws_tiled(M, K)) {
-    // prefill on the DMA-staged kernel: the codes again in its operand order, with the seeds
+  if (!decode && dma_tiled_ok(p, tiled_min_n()) && workspace_bytes >= need + linear_ws_tiled(M, K)) {
+    // prefill on the DMA-staged kernel: x quantized straight into its operand order, with the seeds
     const int64_t Mp = (M + 15) / 16 * 16;
     uint8_t* xt = reinterpret_cast<uint8_t*>(xs) + round256(M * 4);
     float* seeds = reinterpret_cast<float*>(xt + round256(Mp * K));
-    rc = launch_act_tile(xq, K, M, K, xt, seeds, Mp, st);
-    if (rc) return hip_status(rc, "w4a8_linear(act tile)");
+    rc = launch_act_quant_tiled(x, x_dtype, M, K, ldx, xt, xs, seeds, Mp, st);
+    if (rc) return hip_status(rc, "w4a8_linear(act quant, tiled)");
     GemmArgs q = p;
     q.xsrc = nullptr;
     q.xq = xt; q.ldx = K; q.act_scales = xs;
@@ -326,6 +333,8 @@ int w4a8_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, c
     rc = launch_prefill_dma(q, M, 0, st);
     if (rc != kErrUnsupported) return hip_status(rc, "w4a8_linear(prefill, tiled)");
   }
+  rc = launch_act_quant(x, x_dtype, M, K, ldx, xq, K, xs, nullptr, st);
+  if (rc) return hip_status(rc, "w4a8_linear(act quant)");
   p.xsrc = nullptr;
   p.xq = xq; p.ldx = K; p.act_scales = xs;
   return run_dense("w4a8_linear", p, kernel, st);
@@ -346,8 +355,7 @@ int w4a8_linear_launch_count(int64_t M, int64_t N, int64_t K, int x_dtype, int s
   if (M == 0) return 0;
   const bool decode = kernel == 1 || (kernel == 0 && M <= kGemvMaxRows);
   p.xsrc = reinterpret_cast<const uint16_t*>(fake); p.ldxs = K; p.xdtype = x_dtype;
-  if (decode) return gemv_can_fuse_quant(p, (M + 15) / 16) ? 1 : 2;
-  return dma_tiled_ok(p) ? 3 : 2;
+  return decode && gemv_can_fuse_quant(p, (M + 15) / 16) ? 1 : 2;
 }
 
 }  // extern "C"

@@ -85,6 +85,87 @@ act_tile_kernel(const uint8_t* __restrict__ q, int64_t ldq, int64_t M, int KT, u
   }
 }
 
+// act_quant_kernel and act_tile_kernel in one launch, for bf16/fp16 rows: one workgroup of 16 waves
+// per 16-row block (grid-stride). Wave w first takes row w's maximum (the act-quant arithmetic: 16-byte
+// chunks, wave_max), then the block's K tiles w, w + 16, ...: lane l quantizes row (l & 15)'s values
+// [16 (l >> 4), +16) and [64 + 16 (l >> 4), +16) of the tile (the row is read a second time, from
+// cache) into the operand-order block and runs the seed MFMA on them, as act_tile_kernel does on
+// act_quant_kernel's codes. Same codes, scales and seeds, bit for bit; no row-major codes.
+__global__ void __launch_bounds__(1024)
+act_quant_tiled_kernel(const uint16_t* __restrict__ x, int64_t ldx, int64_t M, int64_t K, int dtype,
+                       uint8_t* __restrict__ qt, float* __restrict__ scales, float* __restrict__ seeds,
+                       int64_t seeds_ld) {
+  __shared__ float inv_s[16];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int KT = (int)(K / kTileK);
+  const int64_t nblk = (M + 15) / 16;
+  const int r = lane & 15, qd = lane >> 4;
+  for (int64_t blk = blockIdx.x; blk < nblk; blk += gridDim.x) {
+    {
+      const int64_t m = blk * 16 + wave;
+      float amax = 0.f;
+      if (m < M) {  // wave-uniform
+        const uint16_t* xr = x + m * ldx;
+        int64_t k = (int64_t)lane * 8;
+        for (; k + 3 * 512 < K; k += 4 * 512) {
+          const uint4 c0 = *reinterpret_cast<const uint4*>(xr + k);
+          const uint4 c1 = *reinterpret_cast<const uint4*>(xr + k + 512);
+          const uint4 c2 = *reinterpret_cast<const uint4*>(xr + k + 1024);
+          const uint4 c3 = *reinterpret_cast<const uint4*>(xr + k + 1536);
+          amax = fmaxf(amax, fmaxf(fmaxf(amax8(c0, dtype), amax8(c1, dtype)), fmaxf(amax8(c2, dtype), amax8(c3, dtype))));
+        }
+        for (; k < K; k += 512) amax = fmaxf(amax, amax8(*reinterpret_cast<const uint4*>(xr + k), dtype));
+      }
+      const float s = act_row_scale(wave_max(amax));
+      if (lane == 0) {
+        inv_s[wave] = 1.0f / s;
+        if (m < M) scales[m] = s;
+      }
+    }
+    __syncthreads();
+    const int64_t m = blk * 16 + r;
+    const float inv = inv_s[r];
+    const uint16_t* xr = x + (m < M ? m : 0) * ldx;
+    for (int kt = wave; kt < KT; kt += 16) {
+      uint4 half[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int64_t k = (int64_t)kt * kTileK + 64 * h + 16 * qd;
+        float f[16];
+        if (m < M) {
+          unpack8(*reinterpret_cast<const uint4*>(xr + k), dtype, f);
+          unpack8(*reinterpret_cast<const uint4*>(xr + k + 8), dtype, f + 8);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) f[i] = 0.f;
+        }
+        const uint2 c0 = quant8(f, inv), c1 = quant8(f + 8, inv);
+        half[h] = make_uint4(c0.x, c0.y, c1.x, c1.y);
+        *reinterpret_cast<uint4*>(qt + ((blk * KT + kt) * 2 + h) * 1024 + lane * 16) = half[h];
+      }
+      v8i a;
+      a[0] = (int)half[0].x; a[1] = (int)half[0].y; a[2] = (int)half[0].z; a[3] = (int)half[0].w;
+      a[4] = (int)half[1].x; a[5] = (int)half[1].y; a[6] = (int)half[1].z; a[7] = (int)half[1].w;
+      v4f pre = mfma_f8f8(a, splat8(0xB0B0B0B0u), v4f{0.f, 0.f, 0.f, 0.f});
+      asm volatile("" : "+v"(pre));  // the MFMA runs with every lane active, before the lane branch
+      if (r == 0)
+        *reinterpret_cast<float4*>(seeds + (int64_t)kt * seeds_ld + blk * 16 + 4 * qd) =
+            make_float4(pre[0], pre[1], pre[2], pre[3]);
+    }
+    __syncthreads();  // inv_s is rewritten for the next block
+  }
+}
+
+int launch_act_quant_tiled(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx, uint8_t* qt, float* scales,
+                           float* seeds, int64_t seeds_ld, hipStream_t stream) {
+  if (M <= 0) return kOk;
+  const int64_t nblk = (M + 15) / 16;
+  const dim3 g((unsigned)(nblk < 8192 ? nblk : 8192)), b(1024);
+  hipLaunchKernelGGL(act_quant_tiled_kernel, g, b, 0, stream, reinterpret_cast<const uint16_t*>(x), ldx, M, K, dtype,
+                     qt, scales, seeds, seeds_ld);
+  return hipGetLastError() == hipSuccess ? kOk : kErrHip;
+}
+
 int launch_act_tile(const uint8_t* q, int64_t ldq, int64_t M, int64_t K, uint8_t* qt, float* seeds,
                     int64_t seeds_ld, hipStream_t stream) {
   if (M <= 0) return kOk;

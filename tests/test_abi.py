@@ -219,9 +219,7 @@ def test_linear_launch_count(lib):
     assert lib.w4a8_linear_launch_count(4, 4096, 4096, 0, 0, 1, 0, 32, 0, 0) == 2
     assert lib.w4a8_linear_launch_count(4, 24, 128, 0, 0, 0, 0, 128, 0, 0) == -1
     assert b"multiple of 16" in lib.w4a8_last_error()
-    # prefill on wide symmetric int4 weights from 1024 rows: act quant, the operand-order rewrite, GEMM
-    assert lib.w4a8_linear_launch_count(2048, 28672, 4096, 0, 0, 0, 0, 128, 0, 0) == 3
-    assert lib.w4a8_linear_launch_count(1023, 28672, 4096, 0, 0, 0, 0, 128, 0, 0) == 2
-    assert lib.w4a8_linear_launch_count(2048, 6144, 4096, 0, 0, 0, 0, 128, 0, 0) == 2
-    assert lib.w4a8_linear_launch_count(2048, 28672, 4096, 0, 0, 1, 0, 128, 0, 0) == 2  # zero points
-    assert lib.w4a8_linear_launch_count(2048, 28672, 8192, 0, 1, 0, 1, 32, 0, 0) == 2  # MXFP4
+    # prefill: one quant launch (row-major, or straight into the GEMM's operand order) and the GEMM
+    for M, N, zeros, e2 in ((2048, 28672, 0, 0), (1023, 28672, 0, 0), (2048, 6144, 0, 0), (2048, 28672, 1, 0),
+                            (2048, 28672, 0, 1)):
+        assert lib.w4a8_linear_launch_count(M, N, 4096, 0, e2, zeros, e2, 32 if e2 else 128, 0, 0) == 2
