@@ -326,14 +326,16 @@ def test_producer_pair_bit_identical(kernels, dev, M):
     assert torch.equal(base, pre) and torch.equal(base, pre8)
 
 
-@pytest.mark.parametrize("fmt,M,K,N", [("sym", 2048, 4096, 28672), ("sym", 1100, 1024, 16400), ("sym", 300, 1024, 512),
-                                        ("asym", 1100, 1024, 16384), ("mxfp4", 1024, 4096, 1024)])
+@pytest.mark.parametrize("fmt,M,K,N", [("sym", 2048, 4096, 28672), ("sym", 1100, 1024, 16400), ("sym16", 1030, 2048, 16384),
+                                        ("sym", 300, 1024, 512), ("asym", 1100, 1024, 16384), ("mxfp4", 1024, 4096, 1024)])
 def test_prefill_tiled_quant_matches_row_major(kernels, dev, fmt, M, K, N):
     """Wide symmetric int4 prefill calls that quantize x themselves rewrite the codes in the GEMM's
     operand order with the row-sum seeds (a third launch), which the GEMM reads instead of computing;
     callers' own (x_fp8, act_scales) pairs reach the GEMM row by row and it computes the seeds. Both
     give the same bits (also on a ragged 1025-strip weight and the row-major formats beside them)."""
     x = synth.activations(M, K, seed=M + K, outliers=True).to(dev)
+    if fmt == "sym16":  # fp16 activations (scale rows, codes and seeds from fp16 values)
+        x = x.to(torch.float16)
     if fmt == "mxfp4":
         w, s = synth.mxfp4_weight(N, K, seed=N + 1)
         z, g, e2 = None, 32, True

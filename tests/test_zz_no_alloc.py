@@ -61,3 +61,19 @@ def test_noalloc_matches_workspace_entry(kernels, dev, K, N, g, asym):
                 ref_s = kernels.w4a8_linear_silu(x, tiles, sd, zd, g)
                 torch.cuda.synchronize()
                 assert torch.equal(got_s, ref_s), f"M={M}: noalloc silu differs"
+
+@pytest.mark.gpu
+def test_noalloc_wide_prefill_matches_workspace_entry(kernels, dev):
+    """Wide symmetric int4 prefill: with room in the static scratch the call quantizes into the
+    GEMM's operand order as w4a8_linear does (1100 rows); where only the row-major codes fit (8192
+    x 4096: 33.5 MB of codes, twice that with the operand-order copy) it runs the row-major GEMM.
+    Both equal w4a8_linear with a torch workspace bit for bit, twice in a row."""
+    lib = _lib()
+    for M, K, N in ((1100, 1024, 16384), (8192, 4096, 16384), (1100, 1024, 16384)):
+        w, s, _ = synth.int4_weight(N, K, 128, seed=N + K, asym=False)
+        tiles, sd = kernels.repack_w4(w.to(dev)), s.to(dev)
+        x = synth.activations(M, K, seed=M, outliers=True).to(dev)
+        got = _noalloc(lib, x, tiles, sd, None, 128, N)
+        ref = kernels.w4a8_linear(x, tiles, sd, None, 128)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref), f"M={M} K={K}: noalloc differs from w4a8_linear"
