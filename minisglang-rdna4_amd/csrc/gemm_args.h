@@ -58,7 +58,7 @@ struct GemmArgs {
   // 1: rows 2m and 2m+1 are the two fp8 terms of bf16 activation row m (W4A16): out row m is
   // bf16((0 + y[2m]) + y[2m+1]), silu applied to those sums (prefill DMA kernel only)
   int tsum2;
-  // 1 (dense prefill DMA kernel): xq holds the fp8 codes in MFMA operand order (act_quant_tile_kernel:
+  // 1 (dense prefill DMA kernel): xq holds the fp8 codes in MFMA operand order (act_quant_tiled_kernel, act_tile_kernel:
   // per 16-row block and K tile one 2 KiB block, the block at ((row/16) * KT + kt) * 2048), and for
   // symmetric int4 seeds[kt * seeds_ld + row] holds the row-sum seed MFMA's result for that block
   int a_tiled;
