@@ -286,11 +286,16 @@ __global__ void __launch_bounds__(512) gemv_walk_kernel(const GemmArgs p, const 
   // ---- outputs: the waves' partial sums added in wave order, times the row scale
   const int per = M * 16;
   const int total = ng * half * per;
+  // e = ((g * half + j) * M + i) * 16 + c with half = 1 (NS is 2 only on the silu arm, whose group
+  // is one gate strip and its up strip: one output strip either way). q / M by a float reciprocal:
+  // q + 1/2 lies at least 1/(2M) >= 1/32 from a multiple of M, and for q < 2^16 the product's
+  // rounding error is below 2^-7, so the truncation is exact (no integer division on the tail)
+  const float inv_m = 1.0f / (float)M;
   for (int e = tid; e < total; e += blockDim.x) {
-    const int g = e / (half * per);
-    const int rem = e - g * half * per;
-    const int j = rem / per;
-    const int i = (rem - j * per) >> 4, c = rem & 15;
+    const int c = e & 15, q = e >> 4;
+    const int g = (int)(((float)q + 0.5f) * inv_m);
+    const int i = q - g * M;
+    constexpr int j = 0;
     int64_t sj;
     if (!strip_of(p.silu, g0 + g, j, half, NS, nstrips, sj)) continue;
     // up to 8 partials read at once; the missing ones add +0, which changes no sum (the running sum
