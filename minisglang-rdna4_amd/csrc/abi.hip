@@ -483,7 +483,7 @@ static int check_align(const char* who, int64_t numel, int64_t E, int block_m, i
   if (block_m <= 0 || block_m % 16) return fail(kErrInvalid, "%s: block_m=%d must be a positive multiple of 16", who, block_m);
   if (P < numel + (E + 1) * (block_m - 1))
     return fail(kErrInvalid, "%s: capacity P=%lld < numel + (E+1)*(block_m-1)", who, (long long)P);
-  if (numel > 0x7fffffff) return fail(kErrInvalid, "%s: too many slots", who);
+  if (numel > 0x7fffffff || P > 0x7fffffff) return fail(kErrInvalid, "%s: slots and padded rows must be below 2^31", who);
   return kOk;
 }
 
@@ -577,6 +577,10 @@ int w4a8_moe_gemm(const uint8_t* a_fp8, int64_t lda, const float* a_scales, int 
   if (rc) return rc;
   if (E <= 0 || E > 512) return fail(kErrUnsupported, "w4a8_moe_gemm: num_experts=%lld outside [1, 512]", (long long)E);
   if (block_m <= 0 || block_m % 16) return fail(kErrInvalid, "w4a8_moe_gemm: block_m=%d must be a multiple of 16", block_m);
+  if (numel < 0 || numel > 0x7fffffff || P > 0x7fffffff)
+    return fail(kErrInvalid, "w4a8_moe_gemm: slots (%lld) and padded rows (%lld) must be below 2^31", (long long)numel,
+                (long long)P);
+  if (a_by_token && top_k <= 0) return fail(kErrInvalid, "w4a8_moe_gemm: top_k=%d must be positive", top_k);
   if (lda < K || lda % 16 || !aligned16(a_fp8)) return fail(kErrInvalid, "w4a8_moe_gemm: A rows must be 16-byte aligned, stride >= K");
   if (out_dtype != kBF16 && out_dtype != kF16 && out_dtype != kF32) return fail(kErrInvalid, "w4a8_moe_gemm: unknown output dtype");
   if (silu && (N % 32 || out_dtype == kF32)) return fail(kErrInvalid, "w4a8_moe_gemm: fused silu needs N %% 32 == 0 and bf16/fp16 output");

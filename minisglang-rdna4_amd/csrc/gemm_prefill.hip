@@ -30,7 +30,7 @@ __device__ __forceinline__ bool prow_source(const GemmArgs& p, int64_t r, int64_
   if (r >= p.M || r >= (int64_t)(*p.ntp)) return false;
   const int64_t slot = p.sorted_ids[r];
   if (slot >= p.num_slots) return false;
-  ar = p.a_by_token ? slot / p.top_k : r;
+  ar = p.a_by_token ? (int64_t)((uint32_t)slot / (uint32_t)p.top_k) : r;  // slots < 2^31
   return true;
 }
 
@@ -62,7 +62,7 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_prefill_kernel(const GemmAr
   int64_t expert = 0;
   if (p.sorted_ids) {
     if (blk_row0 >= (int64_t)(*p.ntp)) return;
-    expert = p.expert_ids[blk_row0 / p.bm];
+    expert = p.expert_ids[(uint32_t)blk_row0 / (uint32_t)p.bm];  // padded rows < 2^31
   }
 
   const uint8_t* arow[RB];

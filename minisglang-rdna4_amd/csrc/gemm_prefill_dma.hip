@@ -78,7 +78,7 @@ gemm_dma_kernel(const GemmArgs p) {
     if ((i >> 3) >= share || v >= used) return;
     bx = v % gx;
     by = v / gx;
-    expert = p.expert_ids[(int64_t)by * BM / p.bm];
+    expert = p.expert_ids[(uint32_t)(by * BM) / (uint32_t)p.bm];  // padded rows < 2^31
   }
   const int64_t blk_row0 = (int64_t)by * BM;
   const int N = (int)p.N, K = (int)p.K, KT = (int)p.KT;

@@ -104,7 +104,7 @@ gemm_nv_kernel(const GemmArgs p) {
   int64_t expert = 0;
   if (p.sorted_ids) {
     if (blk_row0 >= (int64_t)(*p.ntp)) return;
-    expert = p.expert_ids[blk_row0 / p.bm];
+    expert = p.expert_ids[(uint32_t)blk_row0 / (uint32_t)p.bm];  // padded rows < 2^31
   }
   const int N = (int)p.N, K = (int)p.K, KT = (int)p.KT;
   const int nstrips = N / kTileN;

@@ -32,7 +32,7 @@ __device__ __forceinline__ bool row_source(const GemmArgs& p, int64_t r, int64_t
   if (r >= p.M || r >= (int64_t)(*p.ntp)) return false;
   const int64_t slot = p.sorted_ids[r];
   if (slot >= p.num_slots) return false;
-  ar = p.a_by_token ? slot / p.top_k : r;
+  ar = p.a_by_token ? (int64_t)((uint32_t)slot / (uint32_t)p.top_k) : r;  // slots < 2^31
   return true;
 }
 
@@ -232,14 +232,14 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemmArgs p, int tpw) {
   const int64_t sg = xcd_remap((int)blockIdx.x, (int)gridDim.x);
   // routed: the block is slot blockIdx.z (output row slot * bm), its A row the slot's token
   const int64_t m0 = kRoute ? (int64_t)blockIdx.z * p.bm : (int64_t)blockIdx.z * 16;
-  const int64_t tok = kRoute ? (int64_t)blockIdx.z / p.top_k : 0;
+  const int64_t tok = kRoute ? (int64_t)(blockIdx.z / (uint32_t)p.top_k) : 0;
   uint32_t logit_raw[kRoute ? kRoutePer : 1];
   if constexpr (kRoute) route_load<kRoutePer>(p.logits, p.ldtype, tok, p.num_experts, logit_raw);
 
   int64_t expert = 0;
   if (kMayGroup && p.sorted_ids) {
     if (m0 >= (int64_t)(*p.ntp)) return;
-    expert = p.expert_ids[m0 / p.bm];
+    expert = p.expert_ids[(uint32_t)m0 / (uint32_t)p.bm];  // padded rows < 2^31
   }
   // A row of this lane. A row that holds no data reads row 0 instead: an A row only feeds its
   // own output row, which is never stored, and a valid address keeps the loads branch-free.
@@ -587,8 +587,12 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemmArgs p, int tpw) {
   __syncthreads();
 
   const int per = nr * 16;
+  // e = (j * nr + i) * 16 + c; q / nr by a float reciprocal (exact: q + 1/2 lies at least 1/32 from
+  // a multiple of nr <= 16, and q < 2^16 keeps the rounding error below 2^-7)
+  const float inv_nr = 1.0f / (float)nr;
   for (int e = threadIdx.x; e < half * per; e += blockDim.x) {
-    const int j = e / per, i = (e - j * per) >> 4, c = e & 15;
+    const int c = e & 15, q = e >> 4;
+    const int j = (int)(((float)q + 0.5f) * inv_nr), i = q - j * nr;
     int64_t sj;
     if (!strip_of(p.silu, sg, j, half, NSTR, nstrips, sj)) continue;
     if (!rvalid[i]) continue;

@@ -29,7 +29,7 @@ __device__ __forceinline__ bool lrow_source(const GemmArgs& p, int64_t r, int64_
   if (r >= p.M || r >= (int64_t)(*p.ntp)) return false;
   const int64_t slot = p.sorted_ids[r];
   if (slot >= p.num_slots) return false;
-  ar = p.a_by_token ? slot / p.top_k : r;
+  ar = p.a_by_token ? (int64_t)((uint32_t)slot / (uint32_t)p.top_k) : r;  // slots < 2^31
   return true;
 }
 
