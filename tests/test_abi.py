@@ -90,6 +90,15 @@ def test_host_validation_rejects_before_launch(lib):
     assert rc == 2 and b"num_experts" in lib.w4a8_last_error()
     rc = lib.w4a8_moe_align(None, 8, 8, 16, 10, None, None, None, None, None)
     assert rc == 1 and b"capacity" in lib.w4a8_last_error()
+    # the grouped kernels index slots and padded rows in 32 bits: 2^31 of either is refused
+    rc = lib.w4a8_moe_align(None, 8, 8, 16, 1 << 31, None, None, None, None, None)
+    assert rc == 1 and b"2^31" in lib.w4a8_last_error()
+    moe_gemm = lambda numel, top_k, P: lib.w4a8_moe_gemm(  # noqa: E731
+        None, 256, None, 1, None, None, None, numel, top_k, 16, P, None, 8, 64, 256, None, 0, None, 0, 128, None, 0,
+        64, 0, None, 0, 0, None)
+    assert moe_gemm(8, 2, 1 << 31) == 1 and b"2^31" in lib.w4a8_last_error()
+    assert moe_gemm(1 << 31, 2, 4096) == 1 and b"2^31" in lib.w4a8_last_error()
+    assert moe_gemm(8, 0, 4096) == 1 and b"top_k" in lib.w4a8_last_error()
     assert lib.w4a8_tile_bytes(32, 256) == 2 * 2 * 1024
     assert lib.w4a8_tile_bytes(32, 160) == 2 * 2 * 1024
     assert lib.w4a8_moe_padded_capacity(8, 128, 16) == 8 + 129 * 15
