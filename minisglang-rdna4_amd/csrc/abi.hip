@@ -85,11 +85,14 @@ static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 static const int kGemvMaxRows = 16;
 
 // Dense symmetric int4 prefill calls of at least W4A8_PREFILL_TILED rows (default 1024; 0 turns it
-// off) on weights of at least 16384 output channels that the DMA-staged kernel takes (its own
-// checks, launch_prefill_dma): their codes are rewritten in that kernel's operand order with the
-// row-sum seeds, which it then reads instead of computing them (act_tile_kernel). The rewrite costs a
-// launch and a pass over the codes; what it saves grows with the column tiles that read each row
-// block (M=2048 / 8192, K=4096: N=28672 5-7% faster, N=4096 and 6144 1-5% slower).
+// off) that the DMA-staged kernel takes (its own checks, launch_prefill_dma) have their codes in
+// that kernel's operand order with the row-sum seeds, which it then reads instead of computing them.
+// w4a8_linear quantizes x straight into that order (act_quant_tiled_lds_kernel, one launch as the
+// row-major quant) on weights of at least W4A8_PREFILL_TILED_N output channels (default 2048:
+// M=8192 qkv 299 -> 279 us, o_proj 205 -> 193, down 711 -> 695, gate_up unchanged within the runs'
+// spread, M=2048 within +-1% but o_proj 58.6 -> 56.6); the producer pair (w4a8_gemm) needs a rewrite
+// launch of the caller's codes (act_tile_kernel), which pays only on weights of 16384+ channels
+// (M=2048 / 8192, K=4096: N=28672 5-7% faster, N=4096 and 6144 1-5% slower).
 static int64_t tiled_min_rows() {
   static const int64_t min_rows = [] {
     const char* e = getenv("W4A8_PREFILL_TILED");
@@ -100,7 +103,7 @@ static int64_t tiled_min_rows() {
 static int64_t tiled_min_n() {
   static const int64_t n = [] {
     const char* e = getenv("W4A8_PREFILL_TILED_N");
-    return e ? (int64_t)atoll(e) : (int64_t)16384;
+    return e ? (int64_t)atoll(e) : (int64_t)2048;
   }();
   return n;
 }

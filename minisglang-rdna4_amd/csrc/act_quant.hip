@@ -156,9 +156,95 @@ act_quant_tiled_kernel(const uint16_t* __restrict__ x, int64_t ldx, int64_t M, i
   }
 }
 
+// act_quant_tiled_kernel's outputs for rows of up to 4096 elements, with x read once: wave w holds row
+// w of the block in registers (lane l: the 8-element chunks l + 64 i), takes its maximum with wave_max,
+// quantizes it (the act-quant arithmetic) and writes each chunk's 8 codes to its operand-order place
+// in LDS; after one barrier wave w copies the block's K tiles w, w + 16, ... to global memory as 1 KiB
+// runs and runs the seed MFMA on them. The two-pass kernel re-reads each row for its tiles, and with
+// 16 rows of 8 KiB per workgroup those re-reads mostly miss L2 (M=8192 K=4096: 34.7 us against the
+// row-major quant's 17). 16 * K bytes of LDS per workgroup; longer rows (16 chunks per lane spill)
+// keep the two-pass kernel.
+template <int CPL>
+__global__ void __launch_bounds__(1024)
+act_quant_tiled_lds_kernel(const uint16_t* __restrict__ x, int64_t ldx, int64_t M, int64_t K, int dtype,
+                           uint8_t* __restrict__ qt, float* __restrict__ scales, float* __restrict__ seeds,
+                           int64_t seeds_ld) {
+  extern __shared__ __align__(16) unsigned char cb[];  // [KT][2 halves][64 lanes][16 B]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int KT = (int)(K / kTileK);
+  const int nch = (int)(K / 8);  // 16-byte chunks of a row
+  const int64_t nblk = (M + 15) / 16;
+  for (int64_t blk = blockIdx.x; blk < nblk; blk += gridDim.x) {
+    const int64_t m = blk * 16 + wave;
+    const bool mok = m < M;  // wave-uniform; rows past M give zero codes
+    const uint16_t* xr = x + (mok ? m : 0) * ldx;
+    uint4 raw[CPL];
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int c = lane + 64 * i;
+      raw[i] = (mok && c < nch) ? *reinterpret_cast<const uint4*>(xr + (int64_t)c * 8) : make_uint4(0u, 0u, 0u, 0u);
+    }
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) amax = fmaxf(amax, amax8(raw[i], dtype));
+    const float s = act_row_scale(wave_max(amax));
+    const float inv = 1.0f / s;
+    if (lane == 0 && mok) scales[m] = s;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int c = lane + 64 * i;
+      if (c < nch) {
+        float f[8];
+        unpack8(raw[i], dtype, f);
+        // element k = 8c: tile k / 128, half (k % 128) / 64, operand lane row + 16 ((k % 64) / 16), byte k % 16
+        const int k = c * 8, kk = k & 127;
+        const int off = (((k >> 7) * 2 + (kk >> 6)) * 64 + wave + 16 * ((kk & 63) >> 4)) * 16 + (kk & 15);
+        *reinterpret_cast<uint2*>(cb + off) = quant8(f, inv);
+      }
+    }
+    __syncthreads();
+    const int r = lane & 15, qd = lane >> 4;
+    for (int kt = wave; kt < KT; kt += 16) {
+      const uint4 h0 = *reinterpret_cast<const uint4*>(cb + (kt * 2) * 1024 + lane * 16);
+      const uint4 h1 = *reinterpret_cast<const uint4*>(cb + (kt * 2 + 1) * 1024 + lane * 16);
+      uint8_t* dst = qt + (blk * KT + kt) * 2048 + lane * 16;
+      *reinterpret_cast<uint4*>(dst) = h0;
+      *reinterpret_cast<uint4*>(dst + 1024) = h1;
+      v8i a;
+      a[0] = (int)h0.x; a[1] = (int)h0.y; a[2] = (int)h0.z; a[3] = (int)h0.w;
+      a[4] = (int)h1.x; a[5] = (int)h1.y; a[6] = (int)h1.z; a[7] = (int)h1.w;
+      v4f pre = mfma_f8f8(a, splat8(0xB0B0B0B0u), v4f{0.f, 0.f, 0.f, 0.f});
+      asm volatile("" : "+v"(pre));  // the MFMA runs with every lane active, before the lane branch
+      if (r == 0)
+        *reinterpret_cast<float4*>(seeds + (int64_t)kt * seeds_ld + blk * 16 + 4 * qd) =
+            make_float4(pre[0], pre[1], pre[2], pre[3]);
+    }
+    __syncthreads();  // the codes of the next block overwrite cb
+  }
+}
+
+template <int CPL>
+static int launch_act_quant_tiled_lds(const uint16_t* x, int dtype, int64_t M, int64_t K, int64_t ldx, uint8_t* qt,
+                                      float* scales, float* seeds, int64_t seeds_ld, hipStream_t stream) {
+  auto kern = act_quant_tiled_lds_kernel<CPL>;
+  static const hipError_t attr =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, 16 * 4096);
+  (void)attr;
+  const int64_t nblk = (M + 15) / 16;
+  const dim3 g((unsigned)(nblk < 8192 ? nblk : 8192)), b(1024);
+  hipLaunchKernelGGL(kern, g, b, (size_t)(16 * K), stream, x, ldx, M, K, dtype, qt, scales, seeds, seeds_ld);
+  return hipGetLastError() == hipSuccess ? kOk : kErrHip;
+}
+
 int launch_act_quant_tiled(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx, uint8_t* qt, float* scales,
                            float* seeds, int64_t seeds_ld, hipStream_t stream) {
   if (M <= 0) return kOk;
+  const uint16_t* xp = reinterpret_cast<const uint16_t*>(x);
+  const int64_t cpl = (K / 8 + 63) / 64;  // 16-byte chunks per lane for one row
+  if (cpl <= 1) return launch_act_quant_tiled_lds<1>(xp, dtype, M, K, ldx, qt, scales, seeds, seeds_ld, stream);
+  if (cpl <= 2) return launch_act_quant_tiled_lds<2>(xp, dtype, M, K, ldx, qt, scales, seeds, seeds_ld, stream);
+  if (cpl <= 4) return launch_act_quant_tiled_lds<4>(xp, dtype, M, K, ldx, qt, scales, seeds, seeds_ld, stream);
+  if (cpl <= 8) return launch_act_quant_tiled_lds<8>(xp, dtype, M, K, ldx, qt, scales, seeds, seeds_ld, stream);
   const int64_t nblk = (M + 15) / 16;
   const dim3 g((unsigned)(nblk < 8192 ? nblk : 8192)), b(1024);
   hipLaunchKernelGGL(act_quant_tiled_kernel, g, b, 0, stream, reinterpret_cast<const uint16_t*>(x), ldx, M, K, dtype,

@@ -326,13 +326,30 @@ def test_producer_pair_bit_identical(kernels, dev, M):
     assert torch.equal(base, pre) and torch.equal(base, pre8)
 
 
+def _row_major_gemm(q, sc, tiles, s, z, g, N, K, e2, out_dtype):
+    """The prefill GEMM on row-major codes: the C ABI's w4a8_gemm with no workspace (no rewrite into
+    the operand order), so the kernel computes the row-sum seeds itself."""
+    abi = pkg("_abi")
+    lib = abi.load()
+    y = torch.empty((q.shape[0], N), dtype=out_dtype, device=q.device)
+    sfmt = abi.SCALE_F16 if s.dtype == torch.float16 else abi.SCALE_E8M0
+    odt = abi.BF16 if out_dtype == torch.bfloat16 else abi.F16
+    abi.check(lib.w4a8_gemm(abi.ptr(q), K, abi.ptr(sc), q.shape[0], abi.ptr(tiles), N, K, abi.ptr(s), sfmt,
+                            abi.ptr(z), abi.W_E2M1 if e2 else abi.W_INT4, g, abi.ptr(y), odt, N, 0, None, 0,
+                            abi.KERNEL_PREFILL, abi.stream_of(q)), "w4a8_gemm")
+    return y
+
+
 @pytest.mark.parametrize("fmt,M,K,N", [("sym", 2048, 4096, 28672), ("sym", 1100, 1024, 16400), ("sym16", 1030, 2048, 16384),
+                                        ("sym", 1030, 1024, 4096), ("sym", 1100, 5120, 2048), ("sym", 1024, 768, 2048),
                                         ("sym", 300, 1024, 512), ("asym", 1100, 1024, 16384), ("mxfp4", 1024, 4096, 1024)])
 def test_prefill_tiled_quant_matches_row_major(kernels, dev, fmt, M, K, N):
-    """Wide symmetric int4 prefill calls that quantize x themselves rewrite the codes in the GEMM's
-    operand order with the row-sum seeds (a third launch), which the GEMM reads instead of computing;
-    callers' own (x_fp8, act_scales) pairs reach the GEMM row by row and it computes the seeds. Both
-    give the same bits (also on a ragged 1025-strip weight and the row-major formats beside them)."""
+    """Symmetric int4 prefill calls of 1024+ rows on 2048+ output channels that quantize x themselves
+    write the codes in the GEMM's operand order with the row-sum seeds (act_quant_tiled_lds_kernel
+    for K <= 4096, the two-pass act_quant_tiled_kernel above: K=5120 here), which the GEMM reads
+    instead of computing. The same bits as the GEMM on row-major codes computing its own seeds
+    (w4a8_gemm with no workspace), and as the producer pair (rewritten into the operand order on
+    16384+ channels); also on a ragged 1025-strip weight and the formats that stay row-major."""
     x = synth.activations(M, K, seed=M + K, outliers=True).to(dev)
     if fmt == "sym16":  # fp16 activations (scale rows, codes and seeds from fp16 values)
         x = x.to(torch.float16)
@@ -347,8 +364,10 @@ def test_prefill_tiled_quant_matches_row_major(kernels, dev, fmt, M, K, N):
     q, sc = kernels.act_quant(x)
     base = kernels.w4a8_linear(x, tiles, sd, zd, g, weight_is_e2m1=e2)
     pre = kernels.w4a8_linear(x, tiles, sd, zd, g, weight_is_e2m1=e2, x_fp8=q, act_scales=sc)
+    rm = _row_major_gemm(q, sc, tiles, sd, zd, g, N, K, e2, x.dtype)
     _sync()
     assert torch.equal(base, pre), f"{fmt} M={M}: max {(base.float() - pre.float()).abs().max().item():.3e}"
+    assert torch.equal(base, rm), f"{fmt} M={M}: max {(base.float() - rm.float()).abs().max().item():.3e}"
 
 
 def test_dispatch_ledger_records_arms(kernels, dev):
