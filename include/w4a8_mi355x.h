@@ -43,8 +43,9 @@ extern "C" {
 
 /* ABI revision of this header. A client checks w4a8_abi_version() == W4A8_ABI_VERSION at load:
  * revision 3 inserted y_dtype as w4a8_moe_combine's second argument, revision 4 added
- * w4a8_linear_launch_count, w4a8_moe_gelu_tanh_mul and w4a8_moe_gemm2_combine's row_dtype. */
-#define W4A8_ABI_VERSION 4
+ * w4a8_linear_launch_count, w4a8_moe_gelu_tanh_mul and w4a8_moe_gemm2_combine's row_dtype,
+ * revision 5 added w4a8_moe_gemm_quant. */
+#define W4A8_ABI_VERSION 5
 int w4a8_abi_version(void);
 
 /* Message of the calling thread's last failed call. */
@@ -212,6 +213,23 @@ int w4a8_moe_gemm(const uint8_t* a_fp8, int64_t lda, const float* a_scales, int 
                   const void* w_tile, int64_t E, int64_t N, int64_t K, const void* scales, int scale_fmt,
                   const int32_t* zeros, int wfmt, int64_t group_size, void* out, int out_dtype, int64_t ldo, int silu,
                   void* workspace, int64_t workspace_bytes, int kernel, void* stream);
+
+/* Workspace bytes of w4a8_moe_gemm_quant: the codes of (P, K) rows (row-major, or in 16-row blocks of
+ * the DMA GEMM's operand order with one row-sum seed per row and K tile) and P f32 row scales. */
+int64_t w4a8_moe_gemm_quant_workspace_bytes(int64_t P, int64_t K);
+
+/* gemm2 of the grouped FFN on the gemm1 buffer in its activation dtype, as the reference's prefill
+ * gemm2 takes it (fp8_wmma.mmq_fp8_moe_gemm on the bf16/fp16 rows, python/minisgl/quant/kernels.py:
+ * 851-874): a (P, K) bf16/fp16 at padded positions (row stride lda elements, 16-byte aligned) is
+ * quantized per row as w4a8_act_quant does (rows at or past *ntp skipped) into the workspace, then
+ * multiplied as w4a8_moe_gemm with a_by_token = 0 does; the outputs are those of that pair, bit for
+ * bit. On the prefill arm with symmetric int4 weights (groups of 128+, K % 128 == 0, K >= 384) the
+ * codes go straight into the DMA GEMM's operand order with their row-sum seeds. Two launches. */
+int w4a8_moe_gemm_quant(const void* a, int a_dtype, int64_t lda, const int32_t* sorted_ids, const int32_t* expert_ids,
+                        const int32_t* ntp, int64_t numel, int block_m, int64_t P, const void* w_tile, int64_t E,
+                        int64_t N, int64_t K, const void* scales, int scale_fmt, const int32_t* zeros, int wfmt,
+                        int64_t group_size, void* out, int out_dtype, int64_t ldo, void* workspace,
+                        int64_t workspace_bytes, int kernel, void* stream);
 
 /* Top-k weighted combine: out[t] = sum_j topk_w[t, j] * y[inv_pos[t*top_k + j]] in f32 over the slots
  * in order, cast to out_dtype. y rows are f32, or bf16/fp16 (y_dtype), as the reference's unfused gemm2

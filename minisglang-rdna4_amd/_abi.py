@@ -58,6 +58,10 @@ SIGNATURES = {
     "w4a8_moe_gemm": (_c_int, [_vp, _c_i64, _vp, _c_int, _vp, _vp, _vp, _c_i64, _c_int, _c_int, _c_i64,
                                _vp, _c_i64, _c_i64, _c_i64, _vp, _c_int, _vp, _c_int, _c_i64,
                                _vp, _c_int, _c_i64, _c_int, _vp, _c_i64, _c_int, _vp]),
+    "w4a8_moe_gemm_quant_workspace_bytes": (_c_i64, [_c_i64, _c_i64]),
+    "w4a8_moe_gemm_quant": (_c_int, [_vp, _c_int, _c_i64, _vp, _vp, _vp, _c_i64, _c_int, _c_i64, _vp, _c_i64, _c_i64,
+                                     _c_i64, _vp, _c_int, _vp, _c_int, _c_i64, _vp, _c_int, _c_i64, _vp, _c_i64,
+                                     _c_int, _vp]),
     "w4a8_moe_combine": (_c_int, [_vp, _c_int, _c_i64, _vp, _vp, _c_i64, _c_int, _c_i64, _vp, _c_int, _vp]),
     "w4a8_moe_gelu_tanh_mul": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _c_i64, _vp, _c_i64, _vp, _vp]),
     "w4a8_moe_gemm2_combine_supported": (_c_int, [_c_i64, _c_int, _c_int, _c_int, _c_i64, _c_int]),

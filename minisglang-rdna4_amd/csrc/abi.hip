@@ -46,7 +46,7 @@ int launch_act_split(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx
 int launch_act_tile(const uint8_t* q, int64_t ldq, int64_t M, int64_t K, uint8_t* qt, float* seeds,
                     int64_t seeds_ld, hipStream_t stream);
 int launch_act_quant_tiled(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx, uint8_t* qt, float* scales,
-                           float* seeds, int64_t seeds_ld, hipStream_t stream);
+                           float* seeds, int64_t seeds_ld, const int32_t* row_count, hipStream_t stream);
 int launch_tsum(const float* y, int64_t N, int64_t M, int dtype, void* out, int64_t ldo, int silu, hipStream_t st);
 int64_t w4a16_moe_max_inter();
 int launch_moe_silu_split(const float* y, int64_t ldy, const int32_t* inv_pos, int64_t T, int top_k, int64_t I,
@@ -327,7 +327,7 @@ int w4a8_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, c
     const int64_t Mp = (M + 15) / 16 * 16;
     uint8_t* xt = reinterpret_cast<uint8_t*>(xs) + round256(M * 4);
     float* seeds = reinterpret_cast<float*>(xt + round256(Mp * K));
-    rc = launch_act_quant_tiled(x, x_dtype, M, K, ldx, xt, xs, seeds, Mp, st);
+    rc = launch_act_quant_tiled(x, x_dtype, M, K, ldx, xt, xs, seeds, Mp, nullptr, st);
     if (rc) return hip_status(rc, "w4a8_linear(act quant, tiled)");
     GemmArgs q = p;
     q.xsrc = nullptr;
@@ -563,6 +563,72 @@ int w4a8_moe_align(const int32_t* topk_ids, int64_t numel, int64_t E, int block_
                                      (hipStream_t)stream), "moe_align");
 }
 
+// Validation and arguments of a grouped GEMM call (w4a8_moe_gemm, w4a8_moe_gemm_quant).
+static int moe_gemm_setup(const char* who, const uint8_t* a_fp8, int64_t lda, const float* a_scales, int a_by_token,
+                          const int32_t* sorted_ids, const int32_t* expert_ids, const int32_t* ntp, int64_t numel,
+                          int top_k, int block_m, int64_t P, const void* w_tile, int64_t E, int64_t N, int64_t K,
+                          const void* scales, int scale_fmt, const int32_t* zeros, int wfmt, int64_t group_size,
+                          void* out, int out_dtype, int64_t ldo, int silu, int kernel, GemmArgs& p, bool& decode) {
+  int rc = check_weights(who, N, K, scale_fmt, zeros, wfmt, group_size);
+  if (rc) return rc;
+  if (E <= 0 || E > 512) return fail(kErrUnsupported, "%s: num_experts=%lld outside [1, 512]", who, (long long)E);
+  if (block_m <= 0 || block_m % 16) return fail(kErrInvalid, "%s: block_m=%d must be a multiple of 16", who, block_m);
+  if (numel < 0 || numel > 0x7fffffff || P > 0x7fffffff)
+    return fail(kErrInvalid, "%s: slots (%lld) and padded rows (%lld) must be below 2^31", who, (long long)numel,
+                (long long)P);
+  if (a_by_token && top_k <= 0) return fail(kErrInvalid, "%s: top_k=%d must be positive", who, top_k);
+  if (lda < K || lda % 16 || !aligned16(a_fp8)) return fail(kErrInvalid, "%s: A rows must be 16-byte aligned, stride >= K", who);
+  if (out_dtype != kBF16 && out_dtype != kF16 && out_dtype != kF32) return fail(kErrInvalid, "%s: unknown output dtype", who);
+  if (silu && (N % 32 || out_dtype == kF32)) return fail(kErrInvalid, "%s: fused silu needs N %% 32 == 0 and bf16/fp16 output", who);
+  const int64_t nout = silu ? N / 2 : N;
+  if (ldo < nout) return fail(kErrInvalid, "%s: ldo=%lld < output width %lld", who, (long long)ldo, (long long)nout);
+  if (kernel < 0 || kernel > 2) return fail(kErrInvalid, "%s: kernel must be 0, 1 or 2", who);
+  decode = kernel == 1 || (kernel == 0 && block_m < 64);
+  if (!decode && block_m % 64) return fail(kErrInvalid, "%s: the prefill arm needs block_m %% 64 == 0 (got %d)", who, block_m);
+
+  p = GemmArgs{};
+  p.xq = a_fp8; p.ldx = lda; p.act_scales = a_scales; p.M = P;
+  p.N = N; p.K = K; p.KT = (K + 127) / 128;
+  p.wt = reinterpret_cast<const uint4*>(w_tile);
+  p.scales = scales; p.sfmt = scale_fmt; p.zeros = zeros; p.group = (int)group_size; p.wfmt = wfmt;
+  p.sorted_ids = sorted_ids; p.expert_ids = expert_ids; p.ntp = ntp; p.top_k = top_k; p.num_slots = numel;
+  p.bm = block_m; p.a_by_token = a_by_token;
+  p.w_expert_tiles = (N / 16) * p.KT;
+  p.s_expert_stride = (K / group_size) * N;
+  // the NVFP4 global is one f32 per output channel per expert; zero words are (K/g, N/8) per expert
+  p.z_expert_stride = scale_fmt == kScaleE4M3 ? N : (K / group_size) * (N / 8);
+  p.out = out; p.out_dtype = out_dtype; p.ldo = ldo; p.silu = silu;
+  return kOk;
+}
+
+// The grouped GEMM's launch on row-major fp8 rows: the decode GEMV below 64-row blocks, else the
+// MFMA kernels on 64- or 128-row tiles.
+static int moe_gemm_run(const char* who, GemmArgs& p, bool decode, int64_t E, void* workspace,
+                        int64_t workspace_bytes, hipStream_t stream) {
+  const int64_t nblk = moe_max_blocks(p.num_slots, E, p.bm, p.M);
+  if (decode) {
+    const int64_t rb = nblk * p.bm / 16;
+    const size_t need = gemv_workspace_bytes(p.M, p.N, p.K, 1, rb);
+    if (need > 0 && (workspace == nullptr || (size_t)workspace_bytes < need))
+      return fail(kErrInvalid, "%s: decode split-K needs a %zu-byte workspace, got %lld", who, need,
+                  (long long)workspace_bytes);
+    p.partial = reinterpret_cast<float*>(workspace);
+    return hip_status(launch_gemv(p, rb, false, stream), "w4a8_moe_gemm(decode)");
+  }
+  const int bm_rows = p.bm % 128 == 0 ? 128 : 64;
+  int rc = launch_prefill_lds(p, nblk * p.bm, bm_rows, stream);
+  if (rc == kErrUnsupported) rc = launch_prefill(p, nblk * p.bm, bm_rows, stream);
+  return hip_status(rc, "w4a8_moe_gemm(prefill)");
+}
+
+// w4a8_moe_gemm_quant's codes: row-major (P, K), or for the tiled gemm2 the codes of whole 16-row
+// blocks in operand order and one row-sum seed per row and K tile, whichever is larger
+static int64_t moe_quant_code_bytes(int64_t P, int64_t K) {
+  const int64_t Pp = (P + 15) / 16 * 16, KT = (K + 127) / 128;
+  const int64_t rm = round256(P * K), tl = round256(Pp * K) + round256(KT * Pp * 4);
+  return rm > tl ? rm : tl;
+}
+
 int64_t w4a8_moe_gemm_workspace_bytes(int64_t numel, int64_t E, int block_m, int64_t P, int64_t N, int64_t K,
                                       int kernel) {
   const bool decode = kernel == 1 || (kernel == 0 && block_m < 64);
@@ -576,50 +642,59 @@ int w4a8_moe_gemm(const uint8_t* a_fp8, int64_t lda, const float* a_scales, int 
                   const void* w_tile, int64_t E, int64_t N, int64_t K, const void* scales, int scale_fmt,
                   const int32_t* zeros, int wfmt, int64_t group_size, void* out, int out_dtype, int64_t ldo, int silu,
                   void* workspace, int64_t workspace_bytes, int kernel, void* stream) {
-  int rc = check_weights("w4a8_moe_gemm", N, K, scale_fmt, zeros, wfmt, group_size);
-  if (rc) return rc;
-  if (E <= 0 || E > 512) return fail(kErrUnsupported, "w4a8_moe_gemm: num_experts=%lld outside [1, 512]", (long long)E);
-  if (block_m <= 0 || block_m % 16) return fail(kErrInvalid, "w4a8_moe_gemm: block_m=%d must be a multiple of 16", block_m);
-  if (numel < 0 || numel > 0x7fffffff || P > 0x7fffffff)
-    return fail(kErrInvalid, "w4a8_moe_gemm: slots (%lld) and padded rows (%lld) must be below 2^31", (long long)numel,
-                (long long)P);
-  if (a_by_token && top_k <= 0) return fail(kErrInvalid, "w4a8_moe_gemm: top_k=%d must be positive", top_k);
-  if (lda < K || lda % 16 || !aligned16(a_fp8)) return fail(kErrInvalid, "w4a8_moe_gemm: A rows must be 16-byte aligned, stride >= K");
-  if (out_dtype != kBF16 && out_dtype != kF16 && out_dtype != kF32) return fail(kErrInvalid, "w4a8_moe_gemm: unknown output dtype");
-  if (silu && (N % 32 || out_dtype == kF32)) return fail(kErrInvalid, "w4a8_moe_gemm: fused silu needs N %% 32 == 0 and bf16/fp16 output");
-  const int64_t nout = silu ? N / 2 : N;
-  if (ldo < nout) return fail(kErrInvalid, "w4a8_moe_gemm: ldo=%lld < output width %lld", (long long)ldo, (long long)nout);
-  if (kernel < 0 || kernel > 2) return fail(kErrInvalid, "w4a8_moe_gemm: kernel must be 0, 1 or 2");
-  const bool decode = kernel == 1 || (kernel == 0 && block_m < 64);
-  if (!decode && block_m % 64) return fail(kErrInvalid, "w4a8_moe_gemm: the prefill arm needs block_m %% 64 == 0 (got %d)", block_m);
-  if (numel == 0) return kOk;
+  GemmArgs p;
+  bool decode;
+  int rc = moe_gemm_setup("w4a8_moe_gemm", a_fp8, lda, a_scales, a_by_token, sorted_ids, expert_ids, ntp, numel, top_k,
+                          block_m, P, w_tile, E, N, K, scales, scale_fmt, zeros, wfmt, group_size, out, out_dtype, ldo,
+                          silu, kernel, p, decode);
+  if (rc || numel == 0) return rc;
+  return moe_gemm_run("w4a8_moe_gemm", p, decode, E, workspace, workspace_bytes, (hipStream_t)stream);
+}
 
-  GemmArgs p = {};
-  p.xq = a_fp8; p.ldx = lda; p.act_scales = a_scales; p.M = P;
-  p.N = N; p.K = K; p.KT = (K + 127) / 128;
-  p.wt = reinterpret_cast<const uint4*>(w_tile);
-  p.scales = scales; p.sfmt = scale_fmt; p.zeros = zeros; p.group = (int)group_size; p.wfmt = wfmt;
-  p.sorted_ids = sorted_ids; p.expert_ids = expert_ids; p.ntp = ntp; p.top_k = top_k; p.num_slots = numel;
-  p.bm = block_m; p.a_by_token = a_by_token;
-  p.w_expert_tiles = (N / 16) * p.KT;
-  p.s_expert_stride = (K / group_size) * N;
-  // the NVFP4 global is one f32 per output channel per expert; zero words are (K/g, N/8) per expert
-  p.z_expert_stride = scale_fmt == kScaleE4M3 ? N : (K / group_size) * (N / 8);
-  p.out = out; p.out_dtype = out_dtype; p.ldo = ldo; p.silu = silu;
+int64_t w4a8_moe_gemm_quant_workspace_bytes(int64_t P, int64_t K) {
+  if (P < 0 || K <= 0) return -1;
+  return moe_quant_code_bytes(P, K) + round256(P * 4);
+}
+
+int w4a8_moe_gemm_quant(const void* a, int a_dtype, int64_t lda, const int32_t* sorted_ids, const int32_t* expert_ids,
+                        const int32_t* ntp, int64_t numel, int block_m, int64_t P, const void* w_tile, int64_t E,
+                        int64_t N, int64_t K, const void* scales, int scale_fmt, const int32_t* zeros, int wfmt,
+                        int64_t group_size, void* out, int out_dtype, int64_t ldo, void* workspace,
+                        int64_t workspace_bytes, int kernel, void* stream) {
+  const char* who = "w4a8_moe_gemm_quant";
+  if (a_dtype != kBF16 && a_dtype != kF16) return fail(kErrInvalid, "%s: a must be bf16 or fp16 (dtype %d)", who, a_dtype);
+  if (lda < K || lda % 8 || !aligned16(a))
+    return fail(kErrInvalid, "%s: a rows must be 16-byte aligned with stride >= K (lda=%lld)", who, (long long)lda);
+  const int64_t need = w4a8_moe_gemm_quant_workspace_bytes(P, K);
+  if (need < 0 || workspace == nullptr || workspace_bytes < need || !aligned16(workspace))
+    return fail(kErrInvalid, "%s: needs a 16-byte aligned workspace of %lld bytes, got %lld", who, (long long)need,
+                (long long)workspace_bytes);
+  uint8_t* codes = reinterpret_cast<uint8_t*>(workspace);
+  float* xs = reinterpret_cast<float*>(codes + moe_quant_code_bytes(P, K));
+  GemmArgs p;
+  bool decode;
+  int rc = moe_gemm_setup(who, codes, K, xs, 0, sorted_ids, expert_ids, ntp, numel, 1, block_m, P, w_tile, E, N, K,
+                          scales, scale_fmt, zeros, wfmt, group_size, out, out_dtype, ldo, 0, kernel, p, decode);
+  if (rc || numel == 0) return rc;
+  const hipStream_t st = (hipStream_t)stream;
+  // rows that can hold data (the grid bound; *ntp bounds the work on the device)
   const int64_t nblk = moe_max_blocks(numel, E, block_m, P);
-  if (decode) {
-    const int64_t rb = nblk * block_m / 16;
-    const size_t need = gemv_workspace_bytes(P, N, K, 1, rb);
-    if (need > 0 && (workspace == nullptr || (size_t)workspace_bytes < need))
-      return fail(kErrInvalid, "w4a8_moe_gemm: decode split-K needs a %zu-byte workspace, got %lld", need,
-                  (long long)workspace_bytes);
-    p.partial = reinterpret_cast<float*>(workspace);
-    return hip_status(launch_gemv(p, rb, false, (hipStream_t)stream), "w4a8_moe_gemm(decode)");
+  const int64_t rows = nblk * block_m < P ? nblk * block_m : P;
+  const bool sym4 = wfmt == kInt4 && scale_fmt == kScaleF16 && group_size % 128 == 0 && !zeros;
+  if (!decode && sym4 && tiled_min_rows() > 0 && K % 128 == 0 && p.KT >= 3 && N * p.KT * 64 < ((int64_t)1 << 31)) {
+    // the padded rows quantized straight into the DMA GEMM's operand order with the row-sum seeds
+    const int64_t Pp = (P + 15) / 16 * 16;
+    float* seeds = reinterpret_cast<float*>(codes + round256(Pp * K));
+    rc = launch_act_quant_tiled(a, a_dtype, rows, K, lda, codes, xs, seeds, Pp, ntp, st);
+    if (rc) return hip_status(rc, "w4a8_moe_gemm_quant(act quant, tiled)");
+    GemmArgs q = p;
+    q.a_tiled = 1; q.seeds = seeds; q.seeds_ld = Pp;
+    rc = launch_prefill_dma(q, nblk * block_m, block_m % 128 == 0 ? 128 : 64, st);
+    if (rc != kErrUnsupported) return hip_status(rc, "w4a8_moe_gemm_quant(prefill, tiled)");
   }
-  const int bm_rows = block_m % 128 == 0 ? 128 : 64;
-  rc = launch_prefill_lds(p, nblk * block_m, bm_rows, (hipStream_t)stream);
-  if (rc == kErrUnsupported) rc = launch_prefill(p, nblk * block_m, bm_rows, (hipStream_t)stream);
-  return hip_status(rc, "w4a8_moe_gemm(prefill)");
+  rc = launch_act_quant(a, a_dtype, rows, K, lda, codes, K, xs, ntp, st);
+  if (rc) return hip_status(rc, "w4a8_moe_gemm_quant(act quant)");
+  return moe_gemm_run(who, p, decode, E, nullptr, 0, st);
 }
 
 int w4a8_moe_gelu_tanh_mul(const void* y, int dtype, int64_t ldy, int64_t rows, int64_t inter, void* out, int64_t ldo,

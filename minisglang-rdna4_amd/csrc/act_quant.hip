@@ -94,17 +94,22 @@ act_tile_kernel(const uint8_t* __restrict__ q, int64_t ldq, int64_t M, int KT, u
 __global__ void __launch_bounds__(1024)
 act_quant_tiled_kernel(const uint16_t* __restrict__ x, int64_t ldx, int64_t M, int64_t K, int dtype,
                        uint8_t* __restrict__ qt, float* __restrict__ scales, float* __restrict__ seeds,
-                       int64_t seeds_ld) {
+                       int64_t seeds_ld, const int32_t* __restrict__ row_count) {
   __shared__ float inv_s[16];
+  int64_t rows = M;  // a device-side row count (the MoE padded row count) bounds the rows
+  if (row_count) {
+    const int64_t rc = *row_count;
+    rows = rc < M ? rc : M;
+  }
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int KT = (int)(K / kTileK);
-  const int64_t nblk = (M + 15) / 16;
+  const int64_t nblk = (rows + 15) / 16;
   const int r = lane & 15, qd = lane >> 4;
   for (int64_t blk = blockIdx.x; blk < nblk; blk += gridDim.x) {
     {
       const int64_t m = blk * 16 + wave;
       float amax = 0.f;
-      if (m < M) {  // wave-uniform
+      if (m < rows) {  // wave-uniform
         const uint16_t* xr = x + m * ldx;
         int64_t k = (int64_t)lane * 8;
         for (; k + 3 * 512 < K; k += 4 * 512) {
@@ -119,20 +124,20 @@ act_quant_tiled_kernel(const uint16_t* __restrict__ x, int64_t ldx, int64_t M, i
       const float s = act_row_scale(wave_max(amax));
       if (lane == 0) {
         inv_s[wave] = 1.0f / s;
-        if (m < M) scales[m] = s;
+        if (m < rows) scales[m] = s;
       }
     }
     __syncthreads();
     const int64_t m = blk * 16 + r;
     const float inv = inv_s[r];
-    const uint16_t* xr = x + (m < M ? m : 0) * ldx;
+    const uint16_t* xr = x + (m < rows ? m : 0) * ldx;
     for (int kt = wave; kt < KT; kt += 16) {
       uint4 half[2];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int64_t k = (int64_t)kt * kTileK + 64 * h + 16 * qd;
         float f[16];
-        if (m < M) {
+        if (m < rows) {
           unpack8(*reinterpret_cast<const uint4*>(xr + k), dtype, f);
           unpack8(*reinterpret_cast<const uint4*>(xr + k + 8), dtype, f + 8);
         } else {
@@ -168,15 +173,20 @@ template <int CPL>
 __global__ void __launch_bounds__(1024)
 act_quant_tiled_lds_kernel(const uint16_t* __restrict__ x, int64_t ldx, int64_t M, int64_t K, int dtype,
                            uint8_t* __restrict__ qt, float* __restrict__ scales, float* __restrict__ seeds,
-                           int64_t seeds_ld) {
+                           int64_t seeds_ld, const int32_t* __restrict__ row_count) {
   extern __shared__ __align__(16) unsigned char cb[];  // [KT][2 halves][64 lanes][16 B]
+  int64_t rows = M;  // as act_quant_tiled_kernel
+  if (row_count) {
+    const int64_t rc = *row_count;
+    rows = rc < M ? rc : M;
+  }
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int KT = (int)(K / kTileK);
   const int nch = (int)(K / 8);  // 16-byte chunks of a row
-  const int64_t nblk = (M + 15) / 16;
+  const int64_t nblk = (rows + 15) / 16;
   for (int64_t blk = blockIdx.x; blk < nblk; blk += gridDim.x) {
     const int64_t m = blk * 16 + wave;
-    const bool mok = m < M;  // wave-uniform; rows past M give zero codes
+    const bool mok = m < rows;  // wave-uniform; rows past the bound give zero codes
     const uint16_t* xr = x + (mok ? m : 0) * ldx;
     uint4 raw[CPL];
 #pragma unroll
@@ -225,30 +235,31 @@ act_quant_tiled_lds_kernel(const uint16_t* __restrict__ x, int64_t ldx, int64_t 
 
 template <int CPL>
 static int launch_act_quant_tiled_lds(const uint16_t* x, int dtype, int64_t M, int64_t K, int64_t ldx, uint8_t* qt,
-                                      float* scales, float* seeds, int64_t seeds_ld, hipStream_t stream) {
+                                      float* scales, float* seeds, int64_t seeds_ld, const int32_t* row_count,
+                                      hipStream_t stream) {
   auto kern = act_quant_tiled_lds_kernel<CPL>;
   static const hipError_t attr =
       hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, 16 * 4096);
   (void)attr;
   const int64_t nblk = (M + 15) / 16;
   const dim3 g((unsigned)(nblk < 8192 ? nblk : 8192)), b(1024);
-  hipLaunchKernelGGL(kern, g, b, (size_t)(16 * K), stream, x, ldx, M, K, dtype, qt, scales, seeds, seeds_ld);
+  hipLaunchKernelGGL(kern, g, b, (size_t)(16 * K), stream, x, ldx, M, K, dtype, qt, scales, seeds, seeds_ld, row_count);
   return hipGetLastError() == hipSuccess ? kOk : kErrHip;
 }
 
 int launch_act_quant_tiled(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx, uint8_t* qt, float* scales,
-                           float* seeds, int64_t seeds_ld, hipStream_t stream) {
+                           float* seeds, int64_t seeds_ld, const int32_t* row_count, hipStream_t stream) {
   if (M <= 0) return kOk;
   const uint16_t* xp = reinterpret_cast<const uint16_t*>(x);
   const int64_t cpl = (K / 8 + 63) / 64;  // 16-byte chunks per lane for one row
-  if (cpl <= 1) return launch_act_quant_tiled_lds<1>(xp, dtype, M, K, ldx, qt, scales, seeds, seeds_ld, stream);
-  if (cpl <= 2) return launch_act_quant_tiled_lds<2>(xp, dtype, M, K, ldx, qt, scales, seeds, seeds_ld, stream);
-  if (cpl <= 4) return launch_act_quant_tiled_lds<4>(xp, dtype, M, K, ldx, qt, scales, seeds, seeds_ld, stream);
-  if (cpl <= 8) return launch_act_quant_tiled_lds<8>(xp, dtype, M, K, ldx, qt, scales, seeds, seeds_ld, stream);
+  if (cpl <= 1) return launch_act_quant_tiled_lds<1>(xp, dtype, M, K, ldx, qt, scales, seeds, seeds_ld, row_count, stream);
+  if (cpl <= 2) return launch_act_quant_tiled_lds<2>(xp, dtype, M, K, ldx, qt, scales, seeds, seeds_ld, row_count, stream);
+  if (cpl <= 4) return launch_act_quant_tiled_lds<4>(xp, dtype, M, K, ldx, qt, scales, seeds, seeds_ld, row_count, stream);
+  if (cpl <= 8) return launch_act_quant_tiled_lds<8>(xp, dtype, M, K, ldx, qt, scales, seeds, seeds_ld, row_count, stream);
   const int64_t nblk = (M + 15) / 16;
   const dim3 g((unsigned)(nblk < 8192 ? nblk : 8192)), b(1024);
   hipLaunchKernelGGL(act_quant_tiled_kernel, g, b, 0, stream, reinterpret_cast<const uint16_t*>(x), ldx, M, K, dtype,
-                     qt, scales, seeds, seeds_ld);
+                     qt, scales, seeds, seeds_ld, row_count);
   return hipGetLastError() == hipSuccess ? kOk : kErrHip;
 }
 

@@ -458,7 +458,7 @@ static int launch_dma_cfg_at(const GemmArgs& p, int64_t row_tiles, hipStream_t s
   return hipGetLastError() == hipSuccess ? kOk : kErrHip;
 }
 
-// dense calls with p.a_tiled take the tiled-A instantiation; grouped calls never set it
+// dense calls with p.a_tiled take the tiled-A instantiation (grouped ones: launch_dma_modes_grouped)
 template <int WM, int WN, int RB, int NSB, int MODE>
 static int launch_dma_cfg(const GemmArgs& p, int64_t row_tiles, hipStream_t stream) {
   if (p.a_tiled) return launch_dma_cfg_at<WM, WN, RB, NSB, MODE, true>(p, row_tiles, stream);
@@ -471,9 +471,11 @@ static int launch_dma_modes(const GemmArgs& p, int mode, int64_t row_tiles, hipS
   if (mode == kPAsym) return launch_dma_cfg<WM, WN, RB, NSB, kPAsym>(p, row_tiles, stream);
   return launch_dma_cfg<WM, WN, RB, NSB, kPE8M0>(p, row_tiles, stream);
 }
-// grouped tiles (row-major A gathered through the sorted ids): no tiled-A instantiation
+// grouped tiles: A rows gathered through the sorted ids, or (p.a_tiled, symmetric int4, A rows at
+// their padded positions: gemm2) the padded rows' codes in operand order with their seeds
 template <int WM, int WN, int RB, int NSB>
 static int launch_dma_modes_grouped(const GemmArgs& p, int mode, int64_t row_tiles, hipStream_t stream) {
+  if (mode == kPSym && p.a_tiled) return launch_dma_cfg_at<WM, WN, RB, NSB, kPSym, true>(p, row_tiles, stream);
   if (mode == kPSym) return launch_dma_cfg_at<WM, WN, RB, NSB, kPSym>(p, row_tiles, stream);
   if (mode == kPAsym) return launch_dma_cfg_at<WM, WN, RB, NSB, kPAsym>(p, row_tiles, stream);
   return launch_dma_cfg_at<WM, WN, RB, NSB, kPE8M0>(p, row_tiles, stream);
@@ -505,7 +507,7 @@ int launch_prefill_dma(const GemmArgs& p, int64_t rows_to_cover, int bm_rows, hi
   // in LDS and its accumulators are the only per-step state, so it takes 64 x 128 wave tiles
   // (256 x 256 per workgroup: a quarter less LDS read per MFMA than 64 x 64); int4 holds the
   // unpacked fp8 weights plus the partials of its per-group scaling and stays at 64 x 64.
-  if (p.a_tiled && (p.sorted_ids || bm_rows)) return kErrUnsupported;
+  if (p.a_tiled && (mode != kPSym || (p.sorted_ids ? p.a_by_token != 0 : bm_rows != 0))) return kErrUnsupported;
   if (bm_rows == 64) return launch_dma_modes_grouped<2, 4, 2, 2>(p, mode, (rows_to_cover + 63) / 64, stream);
   if (bm_rows == 128) return launch_dma_modes_grouped<2, 4, 4, 4>(p, mode, (rows_to_cover + 127) / 128, stream);
   // Grids of at most half a workgroup per CU take smaller tiles. int4: 128 x 128 when that gives

@@ -865,21 +865,21 @@ def _moe_forward(x, w13, w13_scales, w13_zeros, w2, w2_scales, w2_zeros, gating_
                 "sorted_ids": sorted_ids, "expert_ids": expert_ids, "ntp": ntp, "inv_pos": inv, "block_m": block_m,
                 "fused_gemm2": True, "round_y2": round_y2}
 
-    # gemm2 input: per-row fp8 re-quant of the (P, inter) buffer, rows bounded by ntp on device
-    q2 = torch.empty((P, inter), dtype=torch.uint8, device=x.device)
-    s2 = torch.empty((P,), dtype=torch.float32, device=x.device)
-    # rows that can hold data: every expert with slots pads to whole blocks, so ntp <= this bound;
-    # the kernel reads ntp on the device and skips the rest, the bound only sizes the grid
-    rows = min(P, (numel // block_m + min(E, numel)) * block_m)
-    _abi.check(lib.w4a8_act_quant(_abi.ptr(buf2), _abi.dtype_code(x.dtype), rows, inter, inter, _abi.ptr(q2), inter,
-                                  _abi.ptr(s2), _abi.ptr(ntp), _abi.stream_of(x)), "w4a8_moe act_quant(gemm2)")
-    # gemm2's (P, K) rows in the dtype the reference hands them over in (above); the combine sums
-    # them in f32
+    # gemm2 on the (P, inter) buffer in x's dtype, as the reference's prefill gemm2 takes it
+    # (kernels.py:851-874): per-row fp8 re-quant (rows bounded by ntp on the device) into a workspace,
+    # then the grouped GEMM; gemm2's (P, K) rows in the dtype the reference hands them over in
+    # (above), which the combine sums in f32
     ydt = row_dt if y2_dtype is None else y2_dtype
     y2 = torch.empty((P, K), dtype=ydt, device=x.device)
     engaged(f"w4a8_mi355x.moe_gemm2({arm_name}{e2})")
-    _moe_gemm(q2, inter, s2, 0, sorted_ids, expert_ids, ntp, numel, top_k, block_m, P, t2, E, K, inter,
-              w2s, s2f, w2z, wfmt, _grp2, y2, _abi.dtype_code(ydt), K, False, arm, "w4a8_moe gemm2")
+    ws_bytes = int(lib.w4a8_moe_gemm_quant_workspace_bytes(P, inter))
+    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=x.device)
+    _abi.check(
+        lib.w4a8_moe_gemm_quant(_abi.ptr(buf2), _abi.dtype_code(x.dtype), inter, _abi.ptr(sorted_ids),
+                                _abi.ptr(expert_ids), _abi.ptr(ntp), numel, block_m, P, _abi.ptr(t2), E, K, inter,
+                                _abi.ptr(w2s), s2f, _abi.ptr(w2z), wfmt, _grp2, _abi.ptr(y2), _abi.dtype_code(ydt), K,
+                                _abi.ptr(ws), ws_bytes, arm, _abi.stream_of(x)),
+        "w4a8_moe gemm2")
     out = torch.empty((M, K), dtype=x.dtype, device=x.device)
     engaged("w4a8_mi355x.moe_combine")
     _abi.check(lib.w4a8_moe_combine(_abi.ptr(y2), _abi.dtype_code(ydt), K, _abi.ptr(inv), _abi.ptr(topk_weights), M,

@@ -400,6 +400,55 @@ def test_moe_fused_gemm2_combine_bit_exact(kernels, dev, monkeypatch, fmt, T, bm
             assert torch.equal(f["out"], plain["out"]), f"{fmt} T={T} bm={bm}: fused differs, max|d| {dmax:.3e}"
 
 
+@pytest.mark.parametrize("fmt,T,bm,i", [("sym", 512, 128, 768), ("sym", 300, 64, 768), ("sym", 600, 128, 1408),
+                                         ("sym", 200, 128, 5120), ("asym", 512, 128, 768), ("mxfp4", 512, 128, 768),
+                                         ("sym", 16, 16, 768)])
+def test_moe_gemm_quant_matches_quant_then_gemm(kernels, dev, fmt, T, bm, i):
+    """w4a8_moe_gemm_quant (gemm2 on the gemm1 buffer in its activation dtype, the codes straight in
+    the DMA GEMM's operand order with their row-sum seeds on the prefill arm for symmetric int4)
+    gives the bits of w4a8_act_quant + w4a8_moe_gemm on every routed row: 64- and 128-row tiles, the
+    LDS-staged quant (K <= 4096) and the two-pass one (K = 5120), and the row-major arms beside them
+    (zero points, MXFP4, the decode GEMV at block_m 16)."""
+    abi = pkg("_abi")
+    lib = abi.load()
+    e, h, k = 32, 1024, 8
+    _, _, _, w2, s2, z2, e2 = _fmt_experts(fmt, e, h, i, seed=560 + T)
+    t2 = kernels.repack_w4(w2.to(dev), weight_is_e2m1=e2)
+    s2d, z2d = s2.to(dev), None if z2 is None else z2.to(dev)
+    ids = torch.randint(0, e, (T, k), generator=torch.Generator().manual_seed(T), dtype=torch.int32).to(dev)
+    sorted_ids, expert_ids, ntp, _ = kernels._moe_align(ids, e, bm)
+    numel, P = T * k, sorted_ids.numel()
+    a = synth.activations(P, i, seed=570 + T, outliers=True).to(dev)
+    sfmt = abi.SCALE_E8M0 if e2 else abi.SCALE_F16
+    g = i // s2.shape[1]
+    arm = abi.KERNEL_DECODE if bm < 64 else abi.KERNEL_PREFILL
+    # the pair: act quant of the rows below ntp, then the grouped GEMM
+    q = torch.zeros((P, i), dtype=torch.uint8, device=dev)
+    sc = torch.zeros((P,), dtype=torch.float32, device=dev)
+    abi.check(lib.w4a8_act_quant(abi.ptr(a), abi.BF16, P, i, i, abi.ptr(q), i, abi.ptr(sc), abi.ptr(ntp),
+                                 abi.stream_of(a)), "act_quant")
+    ref = torch.zeros((P, h), dtype=torch.bfloat16, device=dev)
+    ws_b = int(lib.w4a8_moe_gemm_workspace_bytes(numel, e, bm, P, h, i, arm))
+    ws = torch.empty((max(ws_b, 1),), dtype=torch.uint8, device=dev)
+    abi.check(lib.w4a8_moe_gemm(abi.ptr(q), i, abi.ptr(sc), 0, abi.ptr(sorted_ids), abi.ptr(expert_ids), abi.ptr(ntp),
+                                numel, k, bm, P, abi.ptr(t2), e, h, i, abi.ptr(s2d), sfmt, abi.ptr(z2d),
+                                abi.W_E2M1 if e2 else abi.W_INT4, g, abi.ptr(ref), abi.BF16, h, 0, abi.ptr(ws), ws_b, arm,
+                                abi.stream_of(a)), "moe_gemm")
+    got = torch.zeros((P, h), dtype=torch.bfloat16, device=dev)
+    wq_b = int(lib.w4a8_moe_gemm_quant_workspace_bytes(P, i))
+    wq = torch.empty((wq_b,), dtype=torch.uint8, device=dev)
+    abi.check(lib.w4a8_moe_gemm_quant(abi.ptr(a), abi.BF16, i, abi.ptr(sorted_ids), abi.ptr(expert_ids), abi.ptr(ntp),
+                                      numel, bm, P, abi.ptr(t2), e, h, i, abi.ptr(s2d), sfmt, abi.ptr(z2d),
+                                      abi.W_E2M1 if e2 else abi.W_INT4, g, abi.ptr(got), abi.BF16, h, abi.ptr(wq), wq_b,
+                                      arm, abi.stream_of(a)), "moe_gemm_quant")
+    _sync()
+    rows = sorted_ids[: int(ntp.item())] < numel  # routed rows (padding rows hold nothing)
+    rows = torch.nonzero(rows).flatten()
+    assert rows.numel() == numel
+    dmax = (got[rows].float() - ref[rows].float()).abs().max().item()
+    assert torch.equal(got[rows], ref[rows]), f"{fmt} T={T} bm={bm} K={i}: max|d| {dmax:.3e}"
+
+
 @pytest.mark.parametrize("fmt", ["sym", "asym", "mxfp4", "nvfp4"])
 @pytest.mark.parametrize("T,e,k,bm,ldt", [(1, 128, 8, 16, torch.float32), (3, 64, 6, 16, torch.bfloat16),
                                           (8, 256, 8, 16, torch.float32), (2, 40, 4, 32, torch.float16)])
