@@ -365,13 +365,18 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemmArgs p, int tpw) {
   const BufRsrc rs_s = make_rsrc(scales, (uint32_t)(ngroups * N * kEsz));
   const BufRsrc rs_z = make_rsrc(zeros, zeros ? (uint32_t)(ngroups * (N / 8) * 4) : 0u);
   const BufRsrc rs_a = make_rsrc(p.xq, 0xffffffffu);
-  const uint32_t a_voff = (uint32_t)((row_ok ? ar : 0) * p.ldx) + 16 * (lane >> 4);
+  // A fragment of tile kt: row-major rows (lane (l & 15)'s row, bytes 16 (l >> 4) and 64 + 16 (l >> 4)
+  // of the tile), or with p.a_tiled (grouped gemm2) the block's operand-order codes, two 1 KiB runs
+  const bool a_t = kMayGroup && p.a_tiled;
+  const uint32_t a_voff = a_t ? (uint32_t)((m0 >> 4) * KT * 2048 + lane * 16)
+                              : (uint32_t)((row_ok ? ar : 0) * p.ldx) + 16 * (lane >> 4);
+  const uint32_t a_step = a_t ? 2048u : (uint32_t)kTileK, a_hi = a_t ? 1024u : 64u;
   // global loads of K tile kt into register slot t: weights, scales, zero words; and the A
   // fragment unless A is staged
   auto load_tile = [&](int t, int kt) {
     if (!kStaged) {
-      const uint4 lo = bload128(rs_a, a_voff, (uint32_t)(kt * kTileK));
-      const uint4 hi = bload128(rs_a, a_voff + 64, (uint32_t)(kt * kTileK));
+      const uint4 lo = bload128(rs_a, a_voff, (uint32_t)kt * a_step);
+      const uint4 hi = bload128(rs_a, a_voff + a_hi, (uint32_t)kt * a_step);
       a[t][0] = (int)lo.x; a[t][1] = (int)lo.y; a[t][2] = (int)lo.z; a[t][3] = (int)lo.w;
       a[t][4] = (int)hi.x; a[t][5] = (int)hi.y; a[t][6] = (int)hi.z; a[t][7] = (int)hi.w;
     }

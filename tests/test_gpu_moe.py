@@ -402,13 +402,16 @@ def test_moe_fused_gemm2_combine_bit_exact(kernels, dev, monkeypatch, fmt, T, bm
 
 @pytest.mark.parametrize("fmt,T,bm,i", [("sym", 512, 128, 768), ("sym", 300, 64, 768), ("sym", 600, 128, 1408),
                                          ("sym", 200, 128, 5120), ("asym", 512, 128, 768), ("mxfp4", 512, 128, 768),
-                                         ("sym", 16, 16, 768)])
+                                         ("sym", 16, 16, 768), ("sym", 256, 16, 768), ("asym", 80, 16, 768),
+                                         ("mxfp4", 64, 16, 1408), ("nvfp4", 64, 16, 768)])
 def test_moe_gemm_quant_matches_quant_then_gemm(kernels, dev, fmt, T, bm, i):
-    """w4a8_moe_gemm_quant (gemm2 on the gemm1 buffer in its activation dtype, the codes straight in
-    the DMA GEMM's operand order with their row-sum seeds on the prefill arm for symmetric int4)
-    gives the bits of w4a8_act_quant + w4a8_moe_gemm on every routed row: 64- and 128-row tiles, the
-    LDS-staged quant (K <= 4096) and the two-pass one (K = 5120), and the row-major arms beside them
-    (zero points, MXFP4, the decode GEMV at block_m 16)."""
+    """w4a8_moe_gemm_quant (gemm2 on the gemm1 buffer in its activation dtype, the rows quantized
+    straight into the MFMA operand order: with their row-sum seeds for the DMA GEMM's symmetric int4
+    tiles, and read as two 1 KiB runs per tile by the decode GEMV of every format) gives the bits of
+    w4a8_act_quant + w4a8_moe_gemm on every routed row: 64- and 128-row tiles, the LDS-staged quant
+    (K <= 4096) and the two-pass one (K = 5120), the row-major MFMA arms (zero points, MXFP4) and
+    the grouped GEMV at block_m 16 for int4 with and without zero points, MXFP4 and NVFP4 (operand
+    order from 16 slots per expert: T of 64+ here, T=16 row-major)."""
     abi = pkg("_abi")
     lib = abi.load()
     e, h, k = 32, 1024, 8
@@ -419,7 +422,7 @@ def test_moe_gemm_quant_matches_quant_then_gemm(kernels, dev, fmt, T, bm, i):
     sorted_ids, expert_ids, ntp, _ = kernels._moe_align(ids, e, bm)
     numel, P = T * k, sorted_ids.numel()
     a = synth.activations(P, i, seed=570 + T, outliers=True).to(dev)
-    sfmt = abi.SCALE_E8M0 if e2 else abi.SCALE_F16
+    sfmt = abi.SCALE_E4M3 if fmt == "nvfp4" else abi.SCALE_E8M0 if e2 else abi.SCALE_F16
     g = i // s2.shape[1]
     arm = abi.KERNEL_DECODE if bm < 64 else abi.KERNEL_PREFILL
     # the pair: act quant of the rows below ntp, then the grouped GEMM
