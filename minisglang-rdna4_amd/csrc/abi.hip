@@ -110,7 +110,8 @@ static int64_t tiled_min_n() {
 static bool dma_tiled_ok(const GemmArgs& p, int64_t min_n = 16384) {
   const int64_t min_rows = tiled_min_rows();
   const bool sym4 = p.wfmt == kInt4 && p.sfmt == kScaleF16 && p.group % 128 == 0 && !p.zeros;
-  return min_rows > 0 && p.M >= min_rows && p.N >= min_n && sym4 && p.K % 128 == 0 && p.KT >= 3 && !(p.silu && (p.N / 16) % 2) &&
+  const bool mx = p.wfmt == kE2M1 && p.sfmt == kScaleE8M0 && p.group == 32;  // MXFP4: A layout only, no seeds
+  return min_rows > 0 && p.M >= min_rows && p.N >= min_n && (sym4 || mx) && p.K % 128 == 0 && p.KT >= 3 && !(p.silu && (p.N / 16) % 2) &&
          p.N * p.KT * 64 < ((int64_t)1 << 31) && p.M * p.K < ((int64_t)1 << 31);
 }
 

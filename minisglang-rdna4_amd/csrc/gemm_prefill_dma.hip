@@ -507,7 +507,8 @@ int launch_prefill_dma(const GemmArgs& p, int64_t rows_to_cover, int bm_rows, hi
   // in LDS and its accumulators are the only per-step state, so it takes 64 x 128 wave tiles
   // (256 x 256 per workgroup: a quarter less LDS read per MFMA than 64 x 64); int4 holds the
   // unpacked fp8 weights plus the partials of its per-group scaling and stays at 64 x 64.
-  if (p.a_tiled && (mode != kPSym || (p.sorted_ids ? p.a_by_token != 0 : bm_rows != 0))) return kErrUnsupported;
+  if (p.a_tiled && (p.sorted_ids ? (mode != kPSym || p.a_by_token != 0) : (bm_rows != 0 || mode == kPAsym)))
+    return kErrUnsupported;
   if (bm_rows == 64) return launch_dma_modes_grouped<2, 4, 2, 2>(p, mode, (rows_to_cover + 63) / 64, stream);
   if (bm_rows == 128) return launch_dma_modes_grouped<2, 4, 4, 4>(p, mode, (rows_to_cover + 127) / 128, stream);
   // Grids of at most half a workgroup per CU take smaller tiles. int4: 128 x 128 when that gives

@@ -342,14 +342,15 @@ def _row_major_gemm(q, sc, tiles, s, z, g, N, K, e2, out_dtype):
 
 @pytest.mark.parametrize("fmt,M,K,N", [("sym", 2048, 4096, 28672), ("sym", 1100, 1024, 16400), ("sym16", 1030, 2048, 16384),
                                         ("sym", 1030, 1024, 4096), ("sym", 1100, 5120, 2048), ("sym", 1024, 768, 2048),
-                                        ("sym", 300, 1024, 512), ("asym", 1100, 1024, 16384), ("mxfp4", 1024, 4096, 1024)])
+                                        ("sym", 300, 1024, 512), ("asym", 1100, 1024, 16384), ("mxfp4", 1024, 4096, 1024),
+                                        ("mxfp4", 1100, 2048, 4096), ("mxfp4", 1024, 1024, 16384)])
 def test_prefill_tiled_quant_matches_row_major(kernels, dev, fmt, M, K, N):
-    """Symmetric int4 prefill calls of 1024+ rows on 2048+ output channels that quantize x themselves
-    write the codes in the GEMM's operand order with the row-sum seeds (act_quant_tiled_lds_kernel
-    for K <= 4096, the two-pass act_quant_tiled_kernel above: K=5120 here), which the GEMM reads
-    instead of computing. The same bits as the GEMM on row-major codes computing its own seeds
-    (w4a8_gemm with no workspace), and as the producer pair (rewritten into the operand order on
-    16384+ channels); also on a ragged 1025-strip weight and the formats that stay row-major."""
+    """Symmetric int4 and MXFP4 prefill calls of 1024+ rows on 2048+ output channels that quantize x
+    themselves write the codes in the GEMM's operand order (act_quant_tiled_lds_kernel for K <= 4096,
+    the two-pass act_quant_tiled_kernel above: K=5120 here), with the row-sum seeds the int4 GEMM
+    reads instead of computing. The same bits as the GEMM on row-major codes (w4a8_gemm with no
+    workspace), and as the producer pair (rewritten into the operand order on 16384+ channels); also
+    on a ragged 1025-strip weight and the formats that stay row-major (zero points, narrow MXFP4)."""
     x = synth.activations(M, K, seed=M + K, outliers=True).to(dev)
     if fmt == "sym16":  # fp16 activations (scale rows, codes and seeds from fp16 values)
         x = x.to(torch.float16)
