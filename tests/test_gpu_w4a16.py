@@ -130,23 +130,24 @@ def test_w4a16_bf16_term_sum_in_epilogue(kernels, dev, fmt):
         assert torch.equal(out, ref), f"{fmt} M={M}: max {(out.float() - ref.float()).abs().max().item():.3e}"
 
 
-def test_w4a16_bf16_term_sum_wide_weights(kernels, dev):
-    """The same on a wide symmetric int4 weight at 600 tokens (1200 term rows): there the terms' codes
-    are also rewritten in the GEMM's operand order with their row-sum seeds before the GEMM, and
-    the fused silu arm runs on the same path."""
+@pytest.mark.parametrize("fmt", ["sym", "mxfp4"])
+def test_w4a16_bf16_term_sum_wide_weights(kernels, dev, fmt):
+    """The same on a wide symmetric int4 or MXFP4 weight at 600 tokens (1200 term rows): there the
+    terms' codes are also rewritten in the GEMM's operand order (with the row-sum seeds for int4)
+    before the GEMM, and the fused silu arm runs on the same path."""
     K, N = 1024, 16384
-    w, s, _, g, _ = _case("sym", N, K, seed=33)
-    tiles, sd = kernels.repack_w4(w.to(dev)), s.to(dev)
+    w, s, _, g, e2 = _case(fmt, N, K, seed=33)
+    tiles, sd = kernels.repack_w4(w.to(dev), weight_is_e2m1=e2), s.to(dev)
     M = 600
     x = (synth.activations(M, K, seed=7, outliers=True, dtype=torch.float32) * 0.5).to(torch.bfloat16).to(dev)
-    out = kernels.w4a16_linear(x, tiles, sd, None, g, N)
+    out = kernels.w4a16_linear(x, tiles, sd, None, g, N, weight_is_e2m1=e2)
     q, sc = kernels.w4a16_act_split(x)
-    y = _split_rows_f32(q, sc, tiles, sd, None, g, N, K, False)
+    y = _split_rows_f32(q, sc, tiles, sd, None, g, N, K, e2)
     ref = ((0.0 + y[0::2]) + y[1::2]).to(torch.bfloat16)
     inter = N // 2
     gh, uh = ref[:, :inter], ref[:, inter:]
     ref_s = (gh.float() / (1.0 + torch.exp(-gh.float()))).to(torch.bfloat16) * uh
-    fused = kernels.w4a16_linear_silu(x, tiles, sd, None, g)
+    fused = kernels.w4a16_linear_silu(x, tiles, sd, None, g, weight_is_e2m1=e2)
     _sync()
     assert torch.equal(out, ref), f"max {(out.float() - ref.float()).abs().max().item():.3e}"
     assert torch.equal(fused, ref_s), f"silu max {(fused.float() - ref_s.float()).abs().max().item():.3e}"
