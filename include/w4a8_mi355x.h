@@ -71,8 +71,8 @@ int w4a8_repack_weights(const int32_t* w_packed, int64_t N, int64_t K, int wfmt,
 /* Workspace bytes w4a8_gemm may use for (M, N, K) and a kernel choice (0 auto, 1 decode, 2 prefill);
  * -1 on bad sizes. Prefill calls of 1024 rows or more on 16384+ output channels: room for the codes
  * rewritten in the GEMM's operand order with one row-sum seed per row and 128 inputs, which symmetric
- * int4 weights take (a launch before the GEMM); without it the GEMM reads the row-major codes, with
- * the same outputs. */
+ * int4 and MXFP4 weights take (a launch before the GEMM); without it the GEMM reads the row-major
+ * codes, with the same outputs. */
 int64_t w4a8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int kernel);
 
 /* Dense W4A8 GEMM: out[m, n] = act_scales[m] * sum_g scale[g, n] * sum_{k in g} e4m3(x[m,k]) * w(n,k).
@@ -88,10 +88,11 @@ int w4a8_gemm(const uint8_t* x_fp8, int64_t ldx, const float* act_scales, int64_
 
 /* Workspace bytes w4a8_linear may need for M rows of K inputs (the fp8 codes and scales of x when
  * they are not produced inside the GEMM kernel; for prefill calls of 1024 rows or more, also the
- * codes again in the GEMM's operand order with one row-sum seed per row and 128 inputs, which wide
- * symmetric int4 weights use); -1 on bad sizes. w4a8_linear also accepts a workspace of just the
- * codes and scales (M * K and 4 * M bytes, each rounded up to 256): such calls run the GEMM on the
- * row-major codes, with the same outputs. */
+ * codes again in the GEMM's operand order with one row-sum seed per row and 128 inputs, which
+ * symmetric int4 and MXFP4 weights of 2048+ output channels use, x quantized straight into it);
+ * -1 on bad sizes. w4a8_linear also accepts a workspace of just the codes and scales (M * K and
+ * 4 * M bytes, each rounded up to 256): such calls run the GEMM on the row-major codes, with the
+ * same outputs. */
 int64_t w4a8_linear_workspace_bytes(int64_t M, int64_t K);
 
 /* Dense W4A8 linear on bf16/fp16 activations x (M, ldx): per-token fp8 quant of x, then the GEMM of
