@@ -343,6 +343,21 @@ def test_moe_block_m_arms_agree(kernels, dev, experts):
         assert rel < 2e-3, rel
 
 
+@pytest.mark.parametrize("T", [48, 512, 1500])
+def test_moe_mfma_tiles_64_and_128_bit_identical(kernels, dev, experts, T):
+    """The MFMA arm's 64- and 128-row tiles run each row with the same arithmetic, so block_m 64
+    and 128 give the same bits: gemm1 (rows gathered by token) and gemm2 (the padded rows in
+    operand order), from mostly-padding blocks (T=48) to mostly-full ones (T=1500)."""
+    w13, s13, w2, s2 = experts
+    x = synth.activations(T, H, seed=455 + T).to(dev)
+    lg = synth.router_logits(T, E, seed=456 + T).to(dev)
+    t13, t2 = kernels.repack_w4(w13.to(dev)), kernels.repack_w4(w2.to(dev))
+    o64, o128 = (kernels.w4a8_moe(x, t13, s13.to(dev), None, t2, s2.to(dev), None, lg, TOPK, True, block_m=bm)
+                 for bm in (64, 128))
+    _sync()
+    assert torch.equal(o64, o128), f"T={T}: max|d| {(o64.float() - o128.float()).abs().max().item():.3e}"
+
+
 def _fmt_experts(fmt, e, h, i, seed):
     """(w13, s13, z13, w2, s2, z2, e2m1) in op layout for one weight format."""
     if fmt in ("sym", "asym"):
