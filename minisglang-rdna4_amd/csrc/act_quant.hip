@@ -54,34 +54,51 @@ act_quant_wave_kernel(const uint16_t* __restrict__ x, int64_t ldx, int64_t M, in
 // instead of 64-byte pieces of 16 rows. With them, per block and K tile, the GEMM's row-sum seed (the
 // e4m3 -0.5 splat MFMA on that operand: the same instruction on the same bytes, so the same bits) at
 // seeds[kt * seeds_ld + row], seeds_ld = M rounded up to 16. Rows past M in the last block are zero
-// codes. One wave per (block, K tile), four per workgroup; every lane active at the MFMA.
+// codes. One wave per (block, 4 K tiles), four per workgroup; every lane active at the MFMA.
 __global__ void __launch_bounds__(256)
 act_tile_kernel(const uint8_t* __restrict__ q, int64_t ldq, int64_t M, int KT, uint8_t* __restrict__ qt,
                 float* __restrict__ seeds, int64_t seeds_ld) {
-  const int lane = threadIdx.x & 63;
+  // A wave takes a 16-row block and 4 consecutive K tiles: it reads the 16 rows' 512 bytes in row
+  // order (two rows per instruction, 16 bytes per lane), stages them in LDS (rows padded to 33
+  // chunks, so the operand reads below hit 16 different bank groups), then writes each tile's two
+  // 1 KiB operand halves and its seeds. A wave per single tile read 16 rows' 64-byte pieces per
+  // instruction and ran at about a third of HBM speed.
+  __shared__ uint4 stg[4][16 * 33];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t nblk = (M + 15) / 16;
-  const int64_t units = nblk * KT;
+  const int KG = (KT + 3) / 4;  // groups of 4 K tiles
+  const int64_t units = nblk * KG;
   const int r = lane & 15, qd = lane >> 4;
-  for (int64_t u = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); u < units; u += (int64_t)gridDim.x * 4) {
-    const int64_t blk = u / KT;
-    const int kt = (int)(u - blk * KT);
-    const int64_t m = blk * 16 + r;
-    const uint8_t* src = q + (m < M ? m : 0) * ldq + (int64_t)kt * kTileK + 16 * qd;
-    const uint4 z = make_uint4(0, 0, 0, 0);
-    const uint4 h0 = m < M ? *reinterpret_cast<const uint4*>(src) : z;
-    const uint4 h1 = m < M ? *reinterpret_cast<const uint4*>(src + 64) : z;
-    uint8_t* dst = qt + u * 2048 + lane * 16;
-    *reinterpret_cast<uint4*>(dst) = h0;
-    *reinterpret_cast<uint4*>(dst + 1024) = h1;
-    v8i a;
-    a[0] = (int)h0.x; a[1] = (int)h0.y; a[2] = (int)h0.z; a[3] = (int)h0.w;
-    a[4] = (int)h1.x; a[5] = (int)h1.y; a[6] = (int)h1.z; a[7] = (int)h1.w;
-    v4f pre = mfma_f8f8(a, splat8(0xB0B0B0B0u), v4f{0.f, 0.f, 0.f, 0.f});
-    asm volatile("" : "+v"(pre));  // the MFMA runs with every lane active, before the lane branch
-    // output lane l holds rows 4 (l >> 4) + i of column l & 15; column 0's lanes store them
-    if (r == 0)
-      *reinterpret_cast<float4*>(seeds + (int64_t)kt * seeds_ld + blk * 16 + 4 * qd) =
-          make_float4(pre[0], pre[1], pre[2], pre[3]);
+  uint4* st = stg[wave];
+  for (int64_t u = (int64_t)blockIdx.x * 4 + wave; u < units; u += (int64_t)gridDim.x * 4) {
+    const int64_t blk = u / KG;
+    const int kt0 = (int)(u - blk * KG) * 4;
+    const int nt = KT - kt0 < 4 ? KT - kt0 : 4;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int rr = 2 * i + (lane >> 5), c = lane & 31;
+      const int64_t m = blk * 16 + rr;
+      const bool ok = m < M && c < nt * 8;
+      st[rr * 33 + c] = ok ? *reinterpret_cast<const uint4*>(q + m * ldq + (int64_t)kt0 * kTileK + c * 16)
+                           : make_uint4(0u, 0u, 0u, 0u);
+    }
+    // the wave reads back only what it wrote: LDS serves one wave's accesses in order
+    for (int t = 0; t < nt; ++t) {
+      const uint4 h0 = st[r * 33 + t * 8 + qd];
+      const uint4 h1 = st[r * 33 + t * 8 + 4 + qd];
+      uint8_t* dst = qt + (blk * KT + kt0 + t) * 2048 + lane * 16;
+      *reinterpret_cast<uint4*>(dst) = h0;
+      *reinterpret_cast<uint4*>(dst + 1024) = h1;
+      v8i a;
+      a[0] = (int)h0.x; a[1] = (int)h0.y; a[2] = (int)h0.z; a[3] = (int)h0.w;
+      a[4] = (int)h1.x; a[5] = (int)h1.y; a[6] = (int)h1.z; a[7] = (int)h1.w;
+      v4f pre = mfma_f8f8(a, splat8(0xB0B0B0B0u), v4f{0.f, 0.f, 0.f, 0.f});
+      asm volatile("" : "+v"(pre));  // the MFMA runs with every lane active, before the lane branch
+      // output lane l holds rows 4 (l >> 4) + i of column l & 15; column 0's lanes store them
+      if (r == 0)
+        *reinterpret_cast<float4*>(seeds + (int64_t)(kt0 + t) * seeds_ld + blk * 16 + 4 * qd) =
+            make_float4(pre[0], pre[1], pre[2], pre[3]);
+    }
   }
 }
 
@@ -355,7 +372,7 @@ int launch_act_tile(const uint8_t* q, int64_t ldq, int64_t M, int64_t K, uint8_t
                     int64_t seeds_ld, hipStream_t stream) {
   if (M <= 0) return kOk;
   const int KT = (int)(K / kTileK);
-  const int64_t units = (M + 15) / 16 * KT;
+  const int64_t units = (M + 15) / 16 * ((KT + 3) / 4);
   const int64_t wgs = (units + 3) / 4;
   const dim3 g((unsigned)(wgs < 65536 ? wgs : 65536)), b(256);
   hipLaunchKernelGGL(act_tile_kernel, g, b, 0, stream, q, ldq, M, KT, qt, seeds, seeds_ld);
