@@ -102,8 +102,8 @@ def test_route_slots_layout(kernels, oracle, dev, monkeypatch, T):
 def test_route_align_quant_bit_exact(kernels, oracle, dev, T, bm):
     """w4a8_moe_route_align with x: route and align equal the oracle's, and x's codes and scales
     equal the act-quant kernel's, bit for bit. T*top_k <= 256 runs as one launch (one workgroup
-    routes and aligns, the others quantize rows; up to 64 slots one wave aligns and the workgroup
-    fills); T = 33 (264 slots) takes the three-launch path."""
+    routes and aligns, the others quantize rows; one wave ranks and places the slots, 64 at a
+    time, and the workgroup fills); T = 33 (264 slots) takes the three-launch path."""
     lg = synth.router_logits(T, E, seed=500 + T)
     x = synth.activations(T, H, seed=T).to(dev)
     x[0] = 0  # a zero row takes the 1e-8 scale floor
@@ -121,10 +121,33 @@ def test_route_align_quant_bit_exact(kernels, oracle, dev, T, bm):
     assert np.array_equal(inv.cpu().numpy()[: T * TOPK], rinv)
 
 
-@pytest.mark.parametrize("E_,k,T", [(64, 6, 5), (256, 4, 8), (256, 4, 100), (512, 2, 7), (512, 16, 40), (20, 3, 9)])
+@pytest.mark.parametrize("T", [20, 32, 40])
+def test_route_align_nan_tokens_dropped(kernels, oracle, dev, T):
+    """Tokens whose logits are all NaN choose no expert (id past E); the align drops their slots as
+    the oracle's align does (not placed, inv_pos -1), on the one-launch path (160 and 256 slots: the
+    one-wave align) and the three-launch one (320 slots)."""
+    lg = synth.router_logits(T, E, seed=520 + T, dtype=torch.float32)
+    lg[1] = float("nan")
+    lg[T - 2] = float("nan")
+    x = synth.activations(T, H, seed=530 + T).to(dev)
+    _, ids, sorted_ids, expert_ids, ntp, inv, _, _ = kernels._route_align_quant(lg.to(dev), TOPK, True, E, 16, x)
+    _sync()
+    ids = ids.cpu().numpy()
+    assert (ids[[1, T - 2]] >= E).all() and (ids[[0, T - 1]] < E).all()
+    rs, re_, rntp, rinv = oracle.moe_align(ids, E, 16)
+    assert int(ntp.item()) == rntp
+    assert np.array_equal(sorted_ids.cpu().numpy(), rs)
+    assert np.array_equal(expert_ids.cpu().numpy(), re_)
+    assert np.array_equal(inv.cpu().numpy()[: T * TOPK], rinv)
+
+
+@pytest.mark.parametrize("E_,k,T", [(64, 6, 5), (256, 4, 8), (256, 4, 100), (512, 2, 7), (512, 16, 40), (20, 3, 9),
+                                    (512, 8, 30), (64, 8, 32), (128, 8, 24), (20, 3, 80), (300, 6, 11)])
 def test_route_align_expert_counts(kernels, oracle, dev, E_, k, T):
     """Expert counts that put 1, 2, 4 or 8 experts on each lane, on both the one-launch path
-    (T*k <= 256) and the route + align kernels; fp32 logits with repeated values (ties)."""
+    (T*k <= 256: one wave ranks the slots in 64-slot chunks, up to all four) and the route + align
+    kernels; fp32 logits with repeated values (ties), and 20 experts for 240 slots (a dozen slots of
+    one expert in a chunk)."""
     g = torch.Generator().manual_seed(E_ + k + T)
     lg = torch.randint(-4, 5, (T, E_), generator=g).float() * 0.25  # many exact ties
     bm = 16
