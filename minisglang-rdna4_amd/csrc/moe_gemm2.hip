@@ -266,14 +266,22 @@ bool moe_gemm2_combine_fits(int64_t K, int scale_fmt, bool has_zeros, int wfmt, 
 // tokens on: each wave quantizes its slot's row once for both and keeps twice the weight bytes in
 // flight (configs[4], whole call: T=8 39.8 -> 38.5 us, T=12 55.7 -> 54.7, T=16 64.0 -> 62.9); below
 // 8 tokens the grid of half as many workgroups leaves CUs idle (T=1 15.5 -> 16.9). Four strips
-// were slower at every T. Each strip's arithmetic is the same, so the bits are too.
+// were slower at every T. Each strip's arithmetic is the same, so the bits are too. K of up to 6
+// tiles (inter 768, the configs[4] experts) takes a 6-tile kernel: the registers of the two tiles
+// the 8-tile one loads and never uses went to occupancy (two strips: 108 -> 88 VGPRs, 4 -> 5 waves
+// per SIMD; T=16 whole call 56.7 -> 54.4 us, T=1..12 within the runs' noise). The tiles past KT
+// are never used either way, so the bits are the same.
 template <int MODE, bool SYM>
 static void g2c_launch(const G2CArgs& a, int64_t T, size_t lds, hipStream_t st) {
   const bool few = a.top_k <= 8;
   const int nstrips = a.N / kTileN;
   const dim3 block((unsigned)(a.top_k * 64));
   auto grid = [&](int nsg) { return dim3((unsigned)((nstrips + nsg - 1) / nsg), (unsigned)T); };
-  if (a.KT <= 8 && few && T >= 8)
+  if (a.KT <= 6 && few && T >= 8)
+    hipLaunchKernelGGL((moe_gemm2_combine_kernel<MODE, SYM, 6, 8, 2>), grid(2), block, lds, st, a);
+  else if (a.KT <= 6 && few)
+    hipLaunchKernelGGL((moe_gemm2_combine_kernel<MODE, SYM, 6, 8, 1>), grid(1), block, lds, st, a);
+  else if (a.KT <= 8 && few && T >= 8)
     hipLaunchKernelGGL((moe_gemm2_combine_kernel<MODE, SYM, 8, 8, 2>), grid(2), block, lds, st, a);
   else if (a.KT <= 8 && few)
     hipLaunchKernelGGL((moe_gemm2_combine_kernel<MODE, SYM, 8, 8, 1>), grid(1), block, lds, st, a);
